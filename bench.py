@@ -1,0 +1,269 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X attention hot path (one GPU).
+
+The headline line measures BASELINE config 2: ragged batched decode attention
+(B=4, per-row KV lengths ~ U[256, 2048], 14 q / 2 kv heads, head_dim 64) over
+24 independent per-layer caches.  One step = the 24 per-layer decode-attention
+launches of one decode token, captured once into a hipGraph and replayed.
+Replicated cache sets (> 256 MB, the MI355X Infinity Cache) are cycled so each
+step reads its K/V from HBM.  ``value`` = algorithmic bytes (valid K/V + q +
+out) per step / step time, in GB/s.
+
+Extra keys report the long-context decode (config 3), the fused
+RoPE+append prefill (config 4) and, when available, the end-to-end
+Qwen2.5-0.5B-shaped decode step (config 5).  ``cpu_baseline`` times the CPU
+oracle on a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+FP16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
+MALL_BYTES = 256 << 20
+
+
+def _args():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--no-extras", action="store_true", help="headline line only")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    return p.parse_args()
+
+
+class GraphStep:
+    """A list of launches captured once into a hipGraph (torch.cuda.CUDAGraph)."""
+
+    def __init__(self, fn):
+        import torch
+
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            fn()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            fn()
+        torch.cuda.synchronize()
+
+    def replay(self):
+        self.graph.replay()
+
+
+def _time_graphs(graphs, steps, warmup):
+    """Replay graphs round-robin; return ms per replay (HIP events on the replay stream)."""
+    import torch
+
+    for i in range(warmup):
+        graphs[i % len(graphs)].replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        graphs[i % len(graphs)].replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def bench_ragged_decode(steps, warmup, dev):
+    """Config 2: 24 per-layer decode-attention launches per step."""
+    import torch
+
+    from qwenforge_amd import ops, workloads
+
+    layers = workloads.decode_ragged_layers(24, 4, seed=0)
+    set_bytes = sum(c.key_cache.numel() * 2 * 2 for c in layers)
+    replicas = max(2, -(-2 * MALL_BYTES // set_bytes))
+    cap_max = max(c.key_cache.shape[2] for c in layers)
+    splits = ops.choose_splits(4, 2, cap_max)
+    flash = ops.make_flash_scratch(4, 2, 7, cap_max, dev, splits=splits)
+    sets = []
+    for _ in range(replicas):
+        sets.append([c.to(dev) for c in layers])
+    kv_last = [torch.tensor([n - 1 for n in c.lengths], dtype=torch.int64, device=dev) for c in layers]
+    outs = [torch.empty(4, 2, 7, 64, dtype=torch.float16, device=dev) for _ in layers]
+
+    def step_fn(cs):
+        def run():
+            for i, c in enumerate(cs):
+                fl = tuple(t if j != 3 else outs[i] for j, t in enumerate(flash))
+                ops.flash_decode_attention(c.grouped, c.key_cache, c.value_cache, c.bias, fl,
+                                           kv_last=kv_last[i])
+        return run
+
+    graphs = [GraphStep(step_fn(cs)) for cs in sets]
+    ms = _time_graphs(graphs, steps, warmup)
+    step_bytes = sum(c.valid_bytes for c in layers)
+    return dict(ms_per_step=ms, step_bytes=step_bytes, launches=len(layers), splits=splits,
+                replicas=replicas, layers=layers)
+
+
+def bench_long_decode(steps, warmup, dev):
+    """Config 3: B=1, L=32768 with 1% of keys x8; caches rotated past the MALL."""
+    import torch
+
+    from qwenforge_amd import ops, workloads
+
+    base = workloads.decode_uniform(1, 32768, seed=0, heavy_frac=0.01)
+    per = base.key_cache.numel() * 2 * 2
+    reps = max(2, -(-2 * MALL_BYTES // per))
+    q = base.grouped.to(dev)
+    ks = [base.key_cache.to(dev) for _ in range(reps)]
+    vs = [base.value_cache.to(dev) for _ in range(reps)]
+    splits = ops.choose_splits(1, 2, 32768)
+    flash = ops.make_flash_scratch(1, 2, 7, 32768, dev, splits=splits)
+    per_graph = 8
+
+    def run_fn(g):
+        def run():
+            for j in range(per_graph):
+                r = (g * per_graph + j) % reps
+                ops.flash_decode_attention(q, ks[r], vs[r], None, flash)
+        return run
+
+    graphs = [GraphStep(run_fn(g)) for g in range(max(1, reps // per_graph))]
+    ms = _time_graphs(graphs, max(1, steps // 8), max(1, warmup // 8)) / per_graph
+    return dict(us_per_layer=ms * 1e3, bytes=base.valid_bytes, splits=splits)
+
+
+def bench_prefill(steps, warmup, dev):
+    """Config 4: causal prefill S=2048 with fused RoPE + cache append."""
+    import torch
+
+    from qwenforge_amd import ops, workloads
+
+    case = workloads.prefill_case(2048, seed=0)
+    c = case.to(dev)
+    kc = torch.zeros(1, 2, 2048, 64, dtype=torch.float16, device=dev)
+    vc = torch.zeros_like(kc)
+    per_graph = 8
+
+    def run():
+        for _ in range(per_graph):
+            ops.gqa_flash_prefill_rope_append(c.query, c.key, c.value, c.cos, c.sin, kc, vc, 0)
+
+    g = GraphStep(run)
+    ms = _time_graphs([g], max(1, steps // 8), max(1, warmup // 8)) / per_graph
+    return dict(us_per_layer=ms * 1e3, flops=case.flops)
+
+
+def cpu_baseline(layers, seconds):
+    """The CPU oracle (fp32 restatement of SE:939-972) on config-2 layers, host cores."""
+    import torch
+
+    import oracle
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    t_end = time.perf_counter() + seconds
+    done_bytes, n_layers, times = 0, 0, []
+    while time.perf_counter() < t_end or n_layers < 3:
+        c = layers[n_layers % len(layers)]
+        t0 = time.perf_counter()
+        oracle.grouped_decode_attention(c.grouped, c.key_cache, c.value_cache, c.bias)
+        times.append(time.perf_counter() - t0)
+        done_bytes += c.valid_bytes
+        n_layers += 1
+    total = sum(times)
+    return {
+        "value": round(done_bytes / total / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{n_layers} config-2 layer calls (B=4 ragged, fp32 oracle), "
+                  f"median {statistics.median(times) * 1e6:.0f} us/layer, {total:.1f} s total",
+    }
+
+
+def main():
+    args = _args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(every box here has one MI355X)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from qwenforge_amd import _lib
+
+    _lib.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    r = bench_ragged_decode(args.steps, args.warmup, dev)
+    ms = r["ms_per_step"]
+    gbs = r["step_bytes"] / (ms * 1e-3) / 1e9
+    us_layer = ms * 1e3 / r["launches"]
+    launch_bytes = r["step_bytes"] / r["launches"]
+    line = {
+        "metric": "flash-decode µs/layer + HBM GB/s (% of peak); decode tok/s at bs=1/4",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded N(0,1) fp16 q/k/v, zero-padded caches, fp16-min bias)",
+        "config": {
+            "workload": "config 2: ragged decode attention, B=4, L_b~U[256,2048], cap=roundup64, "
+                        "14q/2kv heads, hd64, 24 per-layer caches; one step = 24 graph-replayed launches",
+            "global_batch": 4,
+            "kv_lengths_mean": round(sum(sum(c.lengths) for c in r["layers"]) / (4 * 24), 1),
+            "splits": r["splits"],
+            "cache_replicas": r["replicas"],
+        },
+        "us_per_layer": round(us_layer, 3),
+        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(launch_bytes / (us_layer * 1e-6) / 1e9, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(launch_bytes / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "decode_split_kernel<true,true> (fused merge)",
+            "bytes_per_launch": int(launch_bytes),
+            "avg_launch_us": round(us_layer, 3),
+        },
+    }
+    if not args.no_extras:
+        lg = bench_long_decode(args.steps, args.warmup, dev)
+        line["long_decode_cfg3"] = {
+            "us_per_layer": round(lg["us_per_layer"], 3),
+            "GBps": round(lg["bytes"] / (lg["us_per_layer"] * 1e-6) / 1e9, 1),
+            "hbm_frac": round(lg["bytes"] / (lg["us_per_layer"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "splits": lg["splits"],
+        }
+        pf = bench_prefill(args.steps, args.warmup, dev)
+        tf = pf["flops"] / (pf["us_per_layer"] * 1e-6) / 1e12
+        line["prefill_cfg4"] = {
+            "us_per_layer": round(pf["us_per_layer"], 3),
+            "TFLOPs": round(tf, 2),
+            "mfma_frac": round(tf / FP16_MFMA_PEAK_TFLOPS, 4),
+        }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline([c for c in r["layers"]], args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,87 @@
+"""ctypes binding of the C ABI in ``include/qf_attn.h``.
+
+The shared object is built in-tree by ``qwenforge_amd.build``.  There is no
+fallback: if it is missing or does not load, every op raises.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().with_name("_qf_attn.so")
+
+_i64, _i32, _f32, _vp = C.c_int64, C.c_int, C.c_float, C.c_void_p
+
+# name -> argument types, in header order.  Every entry point returns int.
+SIGNATURES = {
+    "qf_decode_attn": [
+        _vp, _i64, _i64, _i64,          # q, q_sb, q_sh, q_sg
+        _vp, _i64, _i64, _i64,          # k, k_sb, k_sh, k_sn
+        _vp, _i64, _i64, _i64,          # v, v_sb, v_sh, v_sn
+        _vp, _i64,                      # bias, bias_sb
+        _vp, _i64,                      # kv_last, kv_last_sb
+        _vp, _vp, _vp, _i32,            # acc, m, l, splits
+        _vp,                            # ticket
+        _vp, _i64, _i64, _i64,          # out, o_sb, o_sh, o_sg
+        _i32, _i32, _i32, _i32, _i32,   # B, KVH, G, D, cap
+        _f32, _vp,                      # scale, stream
+    ],
+    "qf_prefill_attn": [
+        _vp, _i64, _i64, _i64,          # q
+        _vp, _i64, _i64, _i64,          # k
+        _vp, _i64, _i64, _i64,          # v
+        _vp, _vp, _i64, _i64,           # cos, sin, cs_sb, cs_sn
+        _vp, _i64, _i64, _i64,          # k_cache
+        _vp, _i64, _i64, _i64,          # v_cache
+        _i64, _i32,                     # start_pos, cap
+        _vp, _i64, _i64, _i64,          # out
+        _i32, _i32, _i32, _i32, _i32,   # B, QH, KVH, S, D
+        _f32, _vp,                      # scale, stream
+    ],
+    "qf_rope_append": [
+        _vp, _i64, _i64,                # q, q_sb, q_sh
+        _vp, _i64, _i64,                # k
+        _vp, _i64, _i64,                # v
+        _vp, _vp, _i64,                 # cos, sin, cs_sb
+        _vp, _i64, _i64, _i64,          # k_cache
+        _vp, _i64, _i64, _i64,          # v_cache
+        _vp,                            # write_index
+        _vp, _i64, _i64,                # q_out
+        _i32, _i32, _i32, _i32, _i32,   # B, QH, KVH, D, cap
+        _vp,                            # stream
+    ],
+    "qf_error_string": [_i32],
+    "qf_abi_version": [],
+}
+
+_lock = threading.Lock()
+_lib: C.CDLL | None = None
+
+
+def load() -> C.CDLL:
+    """Load ``_qf_attn.so`` once; raise ``RuntimeError`` if it is unavailable."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m qwenforge_amd.build` "
+                "(the HIP kernels have no fallback)"
+            )
+        lib = C.CDLL(str(LIB_PATH))
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = C.c_char_p if name == "qf_error_string" else C.c_int
+        _lib = lib
+        return lib
+
+
+def check(code: int, name: str) -> None:
+    """Raise ``RuntimeError`` for a non-zero return code of entry point ``name``."""
+    if code != 0:
+        msg = load().qf_error_string(code).decode()
+        raise RuntimeError(f"{name} failed with code {code}: {msg}")

@@ -1,0 +1,71 @@
+"""Build recipe for the gfx950 attention library ``_qf_attn.so`` (in-tree).
+
+``python -m qwenforge_amd.build`` compiles every HIP source under ``csrc/``
+for gfx950 with hipcc and links ``qwenforge_amd/_qf_attn.so``.  The shared
+object is plain C ABI (``include/qf_attn.h``); Python reaches it through
+ctypes (``qwenforge_amd._lib``).
+"""
+
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+BUILD_DIR = ROOT / "_build"
+LIB_PATH = PKG / "_qf_attn.so"
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+SOURCES = ["decode_attn.hip", "prefill_attn.hip", "rope_append.hip", "capi.cpp"]
+# Packed-fp32 VALU forms are disabled for all device code (they have produced
+# silently wrong results on this hardware pool); hipcc's host pass warns that it
+# does not know the feature, which is harmless.
+DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+COMMON_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", f"-I{ROOT / 'include'}"]
+
+
+def _compile(src: Path, obj: Path, verbose: bool) -> None:
+    cmd = [HIPCC, *COMMON_FLAGS, *DEVICE_FLAGS, "-c", str(src), "-o", str(obj)]
+    if src.suffix == ".cpp":
+        cmd = [HIPCC, "-O3", "-std=c++17", "-fPIC", f"-I{ROOT / 'include'}",
+               "-D__HIP_PLATFORM_AMD__", "-c", str(src), "-o", str(obj)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stdout}\n{res.stderr}")
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile all sources and link the shared library; returns its path."""
+    BUILD_DIR.mkdir(exist_ok=True)
+    objs = []
+    with cf.ThreadPoolExecutor(max_workers=min(4, os.cpu_count() or 1)) as pool:
+        futs = []
+        for name in SOURCES:
+            src = CSRC / name
+            obj = BUILD_DIR / (src.stem + ".o")
+            objs.append(obj)
+            futs.append(pool.submit(_compile, src, obj, verbose))
+        for f in futs:
+            f.result()
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    path = build(verbose="-v" in sys.argv)
+    print(path)

@@ -1,0 +1,15 @@
+// Host-only helpers of the C ABI (no device code).
+#include <hip/hip_runtime_api.h>
+
+#include "../../include/qf_attn.h"
+
+extern "C" const char* qf_error_string(int code) {
+  if (code == QF_OK) return "success";
+  if (code == QF_ERR_INVALID_ARG)
+    return "invalid argument (null pointer, bad size, misaligned pointer or stride)";
+  if (code == QF_ERR_UNSUPPORTED) return "unsupported shape (requires head_dim 64 and 1 <= G <= 16)";
+  if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
+  return "unknown error";
+}
+
+extern "C" int qf_abi_version(void) { return 100; }

@@ -1,0 +1,509 @@
+// Split-K flash-decoding GQA attention for gfx950 (MI355X).
+//
+// Replaces _flash_decode_split_kernel (student_engine.py:32-115),
+// _flash_decode_combine_kernel (:117-162) and their launcher
+// _flash_decode_attention (:834-874).
+//
+// Work split: one workgroup of NW wave64s per (split, batch row b, kv head h);
+// the waves interleave over 32-key tiles of the split's slot range, with the
+// next tile's loads issued before the current tile is computed.  Per tile a
+// wave
+//   1. streams K straight from HBM into MFMA A-operand registers (16-byte
+//      loads, rows permuted so the score tile comes out in P^T order),
+//   2. streams V with coalesced 16-byte loads (8 lanes per 128-byte row) and
+//      transposes it through a private LDS tile with 8-byte writes (the PV
+//      product needs keys in-lane),
+//   3. computes S^T = K Q^T (2 x 2 MFMA 16x16x32), adds scale and bias in the
+//      log2 domain and runs the online softmax on the lane's query column,
+//   4. accumulates O^T += V^T P^T (4 MFMAs, one per 16-wide d slice).
+// The G query heads of a kv group ride the 16 MFMA columns (columns >= G are
+// zero queries whose results are dropped), so K and V are read once per
+// (b, h).  The waves merge through LDS.  Then, by mode:
+//   kDirect   (one split)  the workgroup writes the fp16 output itself;
+//   kPartial  it writes one partial (acc, m, l) in the reference's scratch
+//             layout and a second kernel merges them (the reference's
+//             two-launch shape);
+//   kFused    it writes the partial with write-through (sc1) stores and takes
+//             a device-scope ticket; the last workgroup of each group of 16
+//             splits merges its group in place into the group's first split,
+//             and the last group merger writes the output and re-arms the
+//             tickets.  Write-through stores plus a wait for their completion
+//             replace an agent-scope release fence, which on this part writes
+//             back the whole L2 per workgroup.
+// Every merge is one pass of independent loads spread over the whole
+// workgroup, so each level costs one dependent memory round trip.
+#include "qf_common.h"
+#include "../../include/qf_attn.h"
+
+namespace qf {
+
+constexpr int kD = 64;
+constexpr int kTile = 32;       // keys per wave iteration
+constexpr int kVtStride = 36;   // LDS row stride (halves) of a transposed V tile
+constexpr int kMaxG = 16;
+constexpr int kGroup = 16;      // splits per first-level merge group
+
+enum Mode { kDirect = 0, kPartial = 1, kFused = 2 };
+
+struct DecodeArgs {
+  const f16* q;
+  int64_t q_sb, q_sh, q_sg;
+  const f16* k;
+  int64_t k_sb, k_sh, k_sn;
+  const f16* v;
+  int64_t v_sb, v_sh, v_sn;
+  const f16* bias;
+  int64_t bias_sb;
+  const int64_t* kv_last;
+  int64_t kv_last_sb;
+  float* acc;
+  float* m;
+  float* l;
+  int32_t* ticket;
+  f16* out;
+  int64_t o_sb, o_sh, o_sg;
+  int B, KVH, G, cap, splits;
+  int bias_vec;      // bias rows are 16-byte aligned: 8 keys per load
+  float scale_log2;  // scale * log2(e)
+};
+
+// Partial-scratch accesses.  kCoherent: relaxed agent-scope atomics, which
+// the compiler emits as write-through / cache-bypassing (sc1) accesses, so a
+// workgroup on another XCD sees them without an L2 writeback.
+template <bool kCoherent>
+__device__ __forceinline__ void st(float* p, float v) {
+  if (kCoherent) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else *p = v;
+}
+template <bool kCoherent>
+__device__ __forceinline__ float ld(const float* p) {
+  if (kCoherent) return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return *p;
+}
+
+// Slot range [lo, hi) of split `s` for batch row `b`.
+__device__ __forceinline__ void split_range(const DecodeArgs& a, int b, int s, int& lo, int& hi) {
+  int upper = a.cap;
+  if (a.kv_last != nullptr) {
+    const int64_t last = a.kv_last[(int64_t)b * a.kv_last_sb];
+    upper = (int)(last + 1 < 0 ? 0 : (last + 1 > a.cap ? a.cap : last + 1));
+  }
+  int split_len = (upper + a.splits - 1) / a.splits;
+  split_len = (split_len + kTile - 1) / kTile * kTile;
+  lo = s * split_len;
+  hi = lo + split_len < upper ? lo + split_len : upper;
+}
+
+// Log-sum-exp merge of `count` partials of (b, h) = bh at split indices
+// first + j*stride, for queries [q0, q0 + nq).  Work item = (query, 4 output
+// dims); the NT threads of the workgroup split each item's partials among
+// `tpi` threads, each folding its share with independent loads (8 at a
+// time), and the shares are combined through LDS.  `final`: write fp16
+// out = acc / l.  Otherwise write the merged partial in place at split
+// `first` (the thread that writes a slice is the only one that read it in
+// this call, and m/l of split `first` are written after the barrier that
+// follows every read).  Every thread of the workgroup must call this.
+template <int NT, bool kCoherent>
+__device__ void merge_parts(const DecodeArgs& a, int bh, int q0, int nq, int first, int stride,
+                            int count, bool final, float* lds) {
+  const int G = a.G;
+  const int items = nq * 16;
+  const int tpi = NT / items;  // threads per item (>= 1: items <= 256 <= NT)
+  const int tid = threadIdx.x;
+  const int item = tid % items, sub = tid / items;
+  const int q = q0 + item / 16, d4 = item % 16;
+  const int64_t pbase = (int64_t)bh * a.splits;
+  float M = kNegInf, L = 0.f;
+  f32x4 A = {0.f, 0.f, 0.f, 0.f};
+  if (sub < tpi) {
+    for (int j0 = sub; j0 < count; j0 += 8 * tpi) {
+      float mv[8], lv[8];
+      f32x4 av[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const int j = j0 + u * tpi;
+        if (j < count) {
+          const int64_t part = pbase + first + (int64_t)j * stride;
+          const float* ap = a.acc + (part * G + q) * kD + 4 * d4;
+          mv[u] = ld<kCoherent>(a.m + part * G + q);
+          lv[u] = ld<kCoherent>(a.l + part * G + q);
+          av[u] = f32x4{ld<kCoherent>(ap), ld<kCoherent>(ap + 1), ld<kCoherent>(ap + 2),
+                        ld<kCoherent>(ap + 3)};
+        } else {
+          mv[u] = kNegInf;
+          lv[u] = 0.f;
+          av[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+      float mc = mv[0];
+#pragma unroll
+      for (int u = 1; u < 8; ++u) mc = fmaxf(mc, mv[u]);
+      const float mn = fmaxf(M, mc);
+      const float safe = (mn == kNegInf) ? 0.f : mn;
+      const float r = (M == kNegInf) ? 0.f : fast_exp2((M - safe) * kLog2e);
+      L *= r;
+      A *= r;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float w = (mv[u] == kNegInf) ? 0.f : fast_exp2((mv[u] - safe) * kLog2e);
+        L += w * lv[u];
+        A += w * av[u];
+      }
+      M = mn;
+    }
+  }
+  // Combine the tpi shares of every item: lds[(sub * items + item) * 6 + ...].
+  if (sub < tpi) {
+    float* e = lds + (sub * items + item) * 6;
+    e[0] = M; e[1] = L; e[2] = A[0]; e[3] = A[1]; e[4] = A[2]; e[5] = A[3];
+  }
+  __syncthreads();
+  if (tid < items) {
+    float Mt = kNegInf;
+    for (int s2 = 0; s2 < tpi; ++s2) Mt = fmaxf(Mt, lds[(s2 * items + item) * 6]);
+    const float safe = (Mt == kNegInf) ? 0.f : Mt;
+    float Lt = 0.f;
+    f32x4 At = {0.f, 0.f, 0.f, 0.f};
+    for (int s2 = 0; s2 < tpi; ++s2) {
+      const float* e = lds + (s2 * items + item) * 6;
+      const float w = (e[0] == kNegInf) ? 0.f : fast_exp2((e[0] - safe) * kLog2e);
+      Lt += w * e[1];
+      At += w * f32x4{e[2], e[3], e[4], e[5]};
+    }
+    if (final) {
+      const float inv = 1.f / Lt;
+      const int b = bh / a.KVH, h = bh % a.KVH;
+      f16x4 o;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) o[c] = (f16)(At[c] * inv);
+      *reinterpret_cast<f16x4*>(a.out + b * a.o_sb + h * a.o_sh + q * a.o_sg + 4 * d4) = o;
+    } else {
+      const int64_t part = pbase + first;
+      float* ap = a.acc + (part * G + q) * kD + 4 * d4;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) st<kCoherent>(ap + c, At[c]);
+      if (d4 == 0) {
+        st<kCoherent>(a.m + part * G + q, Mt);
+        st<kCoherent>(a.l + part * G + q, Lt);
+      }
+    }
+  }
+}
+
+struct Tile {
+  f16x8 k[2][2];  // [score block j][k step kk]
+  f16x8 v[4];     // 4 keys x 8 dims
+};
+
+__device__ __forceinline__ void load_tile(Tile& t, const f16* kb, const f16* vb, int64_t k_sn,
+                                          int64_t v_sn, int t0, int last, int lane) {
+  const int col = lane & 15, grp = lane >> 4;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    // Score-block row r reads key t0 + 8*(r/4) + 4*j + r%4, so C block j holds
+    // keys t0 + 8*grp + 4*j + i in register i: exactly the P^T operand order.
+    int key = t0 + 8 * (col >> 2) + 4 * j + (col & 3);
+    key = key < last ? key : last;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) t.k[j][kk] = load16(kb + (int64_t)key * k_sn + 32 * kk + 8 * grp);
+  }
+  // V: lane (m = lane & 7, c = lane >> 3) reads dims 8c..8c+7 of keys
+  // t0 + 4m + r; the 8 lanes sharing m cover whole 128-byte rows.
+  const int m4 = 4 * (lane & 7), c8 = 8 * (lane >> 3);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    int key = t0 + m4 + r;
+    key = key < last ? key : last;
+    t.v[r] = load16(vb + (int64_t)key * v_sn + c8);
+  }
+}
+
+template <int NW, bool kHasBias, int kMode>
+__global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
+  constexpr int NT = NW * 64;
+  constexpr bool kCoh = kMode == kFused;
+  // LDS: per-wave transposed V tiles during the sweep, reused for the
+  // cross-wave merge and the split merges afterwards.
+  constexpr int kVtBytes = NW * kD * kVtStride * 2;
+  constexpr int kWaveMergeBytes = NW * kMaxG * (kD + 1) * 4;
+  constexpr int kSplitMergeBytes = NT * 6 * 4;
+  constexpr int kA = kVtBytes > kWaveMergeBytes ? kVtBytes : kWaveMergeBytes;
+  constexpr int kLdsBytes = kA > kSplitMergeBytes ? kA : kSplitMergeBytes;
+  __shared__ __attribute__((aligned(16))) unsigned char lds_raw[kLdsBytes];
+  __shared__ float sm_ml[2][NW][kMaxG];
+  __shared__ int sh_last;
+
+  const int s = blockIdx.x;
+  const int bh = blockIdx.y;
+  const int b = bh / a.KVH, h = bh % a.KVH;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
+  const int col = lane & 15;  // query column / A-operand row
+  const int grp = lane >> 4;  // 8-wide k chunk of the operands
+
+  int lo, hi;
+  split_range(a, b, s, lo, hi);
+
+  // Q^T operand: lane holds Q[col][32*kk + 8*grp .. +7].
+  f16x8 qf[2];
+  {
+    const f16* qp = a.q + b * a.q_sb + h * a.q_sh + col * a.q_sg + 8 * grp;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      if (col < a.G) {
+        qf[kk] = load16(qp + 32 * kk);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qf[kk][e] = (f16)0.f;
+      }
+    }
+  }
+
+  float m_run = kNegInf, l_run = 0.f;
+  f32x4 o[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const f16* kb = a.k + b * a.k_sb + h * a.k_sh;
+  const f16* vb = a.v + b * a.v_sb + h * a.v_sh;
+  const f16* biasb = kHasBias ? a.bias + b * a.bias_sb : nullptr;
+  f16(*vt)[kVtStride] = reinterpret_cast<f16(*)[kVtStride]>(lds_raw + w * kD * kVtStride * 2);
+  const int last = hi - 1;
+
+  int t0 = lo + w * kTile;
+  Tile cur, nxt;
+  if (t0 < hi) load_tile(cur, kb, vb, a.k_sn, a.v_sn, t0, last, lane);
+  for (; t0 < hi; t0 += NW * kTile) {
+    const int tn = t0 + NW * kTile;
+    if (tn < hi) load_tile(nxt, kb, vb, a.k_sn, a.v_sn, tn, last, lane);
+
+    // Bias of the lane's 8 keys t0 + 8*grp + jj.
+    float bv[8];
+    const int kbase = t0 + 8 * grp;
+    if (kHasBias) {
+      if (a.bias_vec && kbase + 7 <= last) {
+        const f16x8 b8 = load16(biasb + kbase);
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) bv[jj] = (float)b8[jj] * kLog2e;
+      } else {
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+          const int kc = kbase + jj < last ? kbase + jj : last;
+          bv[jj] = (float)biasb[kc] * kLog2e;
+        }
+      }
+    }
+
+    f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
+    c0 = mfma16x16x32(cur.k[0][0], qf[0], c0);
+    c0 = mfma16x16x32(cur.k[0][1], qf[1], c0);
+    c1 = mfma16x16x32(cur.k[1][0], qf[0], c1);
+    c1 = mfma16x16x32(cur.k[1][1], qf[1], c1);
+
+    // Transpose V into LDS: vt[d][key - t0], four keys per 8-byte write.
+    {
+      const int m4 = 4 * (lane & 7), c8 = 8 * (lane >> 3);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        f16x4 col4 = {cur.v[0][e], cur.v[1][e], cur.v[2][e], cur.v[3][e]};
+        *reinterpret_cast<f16x4*>(&vt[c8 + e][m4]) = col4;
+      }
+    }
+
+    float sc[8];
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      float x = (jj < 4 ? c0[jj] : c1[jj - 4]) * a.scale_log2;
+      if (kHasBias) x += bv[jj];
+      sc[jj] = kbase + jj < hi ? x : kNegInf;
+    }
+    float mt = sc[0];
+#pragma unroll
+    for (int jj = 1; jj < 8; ++jj) mt = fmaxf(mt, sc[jj]);
+    mt = col_max(mt);
+    const float m_new = fmaxf(m_run, mt);
+    const float safe_m = (m_new == kNegInf) ? 0.f : m_new;
+    const float resc = (m_new == kNegInf) ? 1.f : fast_exp2(m_run - m_new);
+    float psum = 0.f;
+    f16x8 pb;
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) {
+      const float p = (sc[jj] == kNegInf) ? 0.f : fast_exp2(sc[jj] - safe_m);
+      psum += p;
+      pb[jj] = (f16)p;
+    }
+    l_run = l_run * resc + psum;
+    m_run = m_new;
+
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const f16x4 va0 = *reinterpret_cast<const f16x4*>(&vt[16 * t + col][8 * grp]);
+      const f16x4 va1 = *reinterpret_cast<const f16x4*>(&vt[16 * t + col][8 * grp + 4]);
+      const f16x8 va = {va0[0], va0[1], va0[2], va0[3], va1[0], va1[1], va1[2], va1[3]};
+      o[t] = mfma16x16x32(va, pb, o[t] * resc);
+    }
+    __builtin_amdgcn_wave_barrier();
+    cur = nxt;
+  }
+
+  l_run = col_sum(l_run);
+
+  // Cross-wave merge through LDS (the V tiles are dead now).
+  __syncthreads();
+  float* sm_o = reinterpret_cast<float*>(lds_raw);  // [NW][16][kD + 1]
+  constexpr int kOStride = kD + 1;
+  if (grp == 0) {
+    sm_ml[0][w][col] = m_run;
+    sm_ml[1][w][col] = l_run;
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sm_o[(w * kMaxG + col) * kOStride + 16 * t + 4 * grp + i] = o[t][i];
+  __syncthreads();
+
+  const int S = a.splits, G = a.G;
+  const int64_t part = (int64_t)bh * S + s;
+  for (int e = tid; e < G * kD; e += NT) {
+    const int q = e / kD, d = e % kD;
+    float mx = kNegInf;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) mx = fmaxf(mx, sm_ml[0][ww][q]);
+    const float safe = (mx == kNegInf) ? 0.f : mx;
+    float so = 0.f, sl = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) {
+      const float mw = sm_ml[0][ww][q];
+      const float wt = (mw == kNegInf) ? 0.f : fast_exp2(mw - safe);
+      so += wt * sm_o[(ww * kMaxG + q) * kOStride + d];
+      sl += wt * sm_ml[1][ww][q];
+    }
+    if (kMode == kDirect) {
+      a.out[b * a.o_sb + h * a.o_sh + q * a.o_sg + d] = (f16)(so / sl);
+    } else {
+      st<kCoh>(a.acc + (part * G + q) * kD + d, so);
+      if (d == 0) {
+        st<kCoh>(a.m + part * G + q, (mx == kNegInf) ? kNegInf : mx * kLn2);
+        st<kCoh>(a.l + part * G + q, sl);
+      }
+    }
+  }
+
+  if (kMode == kFused) {
+    float* lds = reinterpret_cast<float*>(lds_raw);
+    const int ng = (S + kGroup - 1) / kGroup;
+    const int g = s / kGroup;
+    const int gsize = (S - g * kGroup) < kGroup ? (S - g * kGroup) : kGroup;
+    int32_t* tk = a.ticket + (int64_t)bh * (ng + 1);
+    // Wait until this workgroup's write-through stores have completed, then
+    // take a ticket; the workgroup that completes a count merges.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __syncthreads();
+    if (tid == 0) sh_last = (atomicAdd(tk + g, 1) == gsize - 1);
+    __syncthreads();
+    if (!sh_last) return;
+    if (ng == 1) {
+      merge_parts<NT, true>(a, bh, 0, G, 0, 1, S, true, lds);
+      if (tid == 0) atomicExch(tk + g, 0);
+      return;
+    }
+    merge_parts<NT, true>(a, bh, 0, G, g * kGroup, 1, gsize, false, lds);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __syncthreads();
+    if (tid == 0) {
+      atomicExch(tk + g, 0);
+      sh_last = (atomicAdd(tk + ng, 1) == ng - 1);
+    }
+    __syncthreads();
+    if (!sh_last) return;
+    merge_parts<NT, true>(a, bh, 0, G, 0, kGroup, ng, true, lds);
+    if (tid == 0) atomicExch(tk + ng, 0);
+  }
+}
+
+// Second launch of the two-kernel shape: one workgroup per (b, h, query).
+__global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
+  __shared__ float lds[256 * 6];
+  const int bh = blockIdx.x / a.G, q = blockIdx.x % a.G;
+  merge_parts<256, false>(a, bh, q, 1, 0, 1, a.splits, true, lds);
+}
+
+template <int NW, bool kHasBias>
+static void launch_split(const DecodeArgs& a, int mode, dim3 grid, hipStream_t st) {
+  const dim3 block(NW * 64);
+  if (mode == kDirect) hipLaunchKernelGGL((decode_split_kernel<NW, kHasBias, kDirect>), grid, block, 0, st, a);
+  else if (mode == kPartial) hipLaunchKernelGGL((decode_split_kernel<NW, kHasBias, kPartial>), grid, block, 0, st, a);
+  else hipLaunchKernelGGL((decode_split_kernel<NW, kHasBias, kFused>), grid, block, 0, st, a);
+}
+
+template <int NW>
+static void launch_nw(const DecodeArgs& a, int mode, dim3 grid, hipStream_t st) {
+  if (a.bias) launch_split<NW, true>(a, mode, grid, st);
+  else launch_split<NW, false>(a, mode, grid, st);
+}
+
+}  // namespace qf
+
+using namespace qf;
+
+static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Waves per workgroup (measured on MI355X): eight for up to two workgroups
+// per CU, sixteen when only a handful of CUs get work, four for large grids.
+static int pick_waves(int splits, int B, int KVH) {
+  const int64_t wgs = (int64_t)splits * B * KVH;
+  if (wgs <= 16) return 16;
+  if (wgs <= 512) return 8;
+  return 4;
+}
+
+extern "C" int qf_decode_attn(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sg,
+                              const void* k, int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                              const void* v, int64_t v_sb, int64_t v_sh, int64_t v_sn,
+                              const void* bias, int64_t bias_sb,
+                              const int64_t* kv_last, int64_t kv_last_sb,
+                              float* acc, float* m, float* l, int splits,
+                              int32_t* ticket,
+                              void* out, int64_t o_sb, int64_t o_sh, int64_t o_sg,
+                              int B, int KVH, int G, int D, int cap, float scale,
+                              void* stream) {
+  if (D != kD || G < 1 || G > kMaxG) return QF_ERR_UNSUPPORTED;
+  if (!q || !k || !v || !acc || !m || !l || !out) return QF_ERR_INVALID_ARG;
+  if (B < 1 || KVH < 1 || cap < 1 || splits < 1 || splits > 65535 || B * (int64_t)KVH > 65535)
+    return QF_ERR_INVALID_ARG;
+  if ((int64_t)B * KVH * G > 0x7fffffff) return QF_ERR_INVALID_ARG;
+  // 16-byte vector loads of q/k/v rows, 8-byte stores of out.
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v)) return QF_ERR_INVALID_ARG;
+  if ((q_sb | q_sh | q_sg | k_sb | k_sh | k_sn | v_sb | v_sh | v_sn) & 7) return QF_ERR_INVALID_ARG;
+  if (((reinterpret_cast<uintptr_t>(out) & 7u) != 0) || ((o_sb | o_sh | o_sg) & 3)) return QF_ERR_INVALID_ARG;
+
+  DecodeArgs a;
+  a.q = static_cast<const f16*>(q);
+  a.q_sb = q_sb; a.q_sh = q_sh; a.q_sg = q_sg;
+  a.k = static_cast<const f16*>(k);
+  a.k_sb = k_sb; a.k_sh = k_sh; a.k_sn = k_sn;
+  a.v = static_cast<const f16*>(v);
+  a.v_sb = v_sb; a.v_sh = v_sh; a.v_sn = v_sn;
+  a.bias = static_cast<const f16*>(bias);
+  a.bias_sb = bias_sb;
+  a.bias_vec = bias != nullptr && aligned16(bias) && (bias_sb & 7) == 0;
+  a.kv_last = kv_last;
+  a.kv_last_sb = kv_last_sb;
+  a.acc = acc; a.m = m; a.l = l;
+  a.ticket = ticket;
+  a.out = static_cast<f16*>(out);
+  a.o_sb = o_sb; a.o_sh = o_sh; a.o_sg = o_sg;
+  a.B = B; a.KVH = KVH; a.G = G; a.cap = cap; a.splits = splits;
+  a.scale_log2 = scale * kLog2e;
+
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int mode = splits == 1 ? kDirect : (ticket != nullptr ? kFused : kPartial);
+  const dim3 grid(splits, B * KVH);
+  const int nw = pick_waves(splits, B, KVH);
+  if (nw == 16) launch_nw<16>(a, mode, grid, st);
+  else if (nw == 8) launch_nw<8>(a, mode, grid, st);
+  else launch_nw<4>(a, mode, grid, st);
+  if (mode == kPartial) hipLaunchKernelGGL(decode_combine_kernel, dim3(B * KVH * G), dim3(256), 0, st, a);
+  return (int)hipGetLastError();
+}

@@ -1,0 +1,85 @@
+// Shared device helpers for the gfx950 attention kernels.
+//
+// Matrix-core convention used by every kernel in this library: scores are
+// computed transposed, S^T = K * Q^T, and the output as O^T = V^T * P^T, with
+// v_mfma_f32_16x16x32_f16.  Its operand layouts (wave64) are
+//   A (16 x 32):  lane l holds A[l % 16][8*(l/16) .. 8*(l/16)+7]
+//   B (32 x 16):  lane l holds B[8*(l/16) .. 8*(l/16)+7][l % 16]
+//   C (16 x 16):  lane l holds C[4*(l/16) + i][l % 16], i = 0..3
+// so the query index is always the lane's column (l % 16): the softmax
+// statistics of a query live in the four lanes {c, c+16, c+32, c+48}, and the
+// probabilities produced as a C tile feed the P^T operand of the next MFMA
+// without any data movement (see the key permutation in the kernels).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qf {
+
+typedef _Float16 f16;
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kNegInf = -__builtin_huge_valf();
+
+__device__ __forceinline__ f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ f16x8 load16(const f16* p) {
+  return *reinterpret_cast<const f16x8*>(p);
+}
+
+__device__ __forceinline__ void store16(f16* p, f16x8 v) {
+  *reinterpret_cast<f16x8*>(p) = v;
+}
+
+// fp16(x) for an fp32 value, round-to-nearest-even.
+__device__ __forceinline__ float round16(float x) { return (float)(f16)x; }
+
+// Rotate-half RoPE of one 8-element chunk pair with the eager fp16 rounding
+// sequence out = fp16(fp16(x*cos) + fp16(rotate_half(x)*sin)): `lo` holds
+// dims [c, c+8) of the first half, `hi` the matching dims [c+32, c+40) of the
+// second half; rotate_half(x) is -hi on the first half and lo on the second.
+// Contraction is off here: hipcc narrows each rounded product to an fp16
+// multiply and would otherwise fuse product and sum into one fma, skipping the
+// rounding of the second product that the eager sequence performs.
+__device__ __forceinline__ void rope_pair(f16x8& lo, f16x8& hi, f16x8 cos_lo, f16x8 sin_lo,
+                                          f16x8 cos_hi, f16x8 sin_hi) {
+#pragma clang fp contract(off)
+  f16x8 out_lo, out_hi;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float xl = (float)lo[e], xh = (float)hi[e];
+    // fp16(-y) == -fp16(y), so a + fp16(-xh*sin) is written as a - fp16(xh*sin).
+    const float a = round16(xl * (float)cos_lo[e]);
+    const float b = round16(xh * (float)sin_lo[e]);
+    const float c = round16(xh * (float)cos_hi[e]);
+    const float d = round16(xl * (float)sin_hi[e]);
+    out_lo[e] = (f16)(a - b);
+    out_hi[e] = (f16)(c + d);
+  }
+  lo = out_lo;
+  hi = out_hi;
+}
+
+// Reductions over the four lanes that share a query column (l ^ 16, l ^ 32).
+__device__ __forceinline__ float col_max(float x) {
+  x = fmaxf(x, __shfl_xor(x, 16));
+  x = fmaxf(x, __shfl_xor(x, 32));
+  return x;
+}
+
+__device__ __forceinline__ float col_sum(float x) {
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+
+}  // namespace qf

@@ -1,0 +1,339 @@
+"""Torch-facing drop-ins for the reference engine's attention hot path.
+
+Each function keeps the call signature ``student_engine.py`` uses today and
+forwards raw device pointers, strides and the current HIP stream to the C ABI
+(``include/qf_attn.h``).  Nothing here computes on the host: a missing
+library or a CPU tensor raises.
+
+* ``flash_decode_attention(grouped, key_cache, value_cache, attn_bias, flash)``
+  -- ``StudentEngine._flash_decode_attention`` (SE:834-874).
+* ``torch.ops.student_qwen.gqa_flash_prefill(query, key, value)``
+  -- the custom op of SE:254-292 (same name, schema and fake).
+* ``torch.ops.student_qwen.gqa_flash_prefill_rope_append(q, k, v, cos, sin,
+  key_cache, value_cache, start_pos)`` -- prefill with RoPE and the slice
+  append of SE:715-716 fused in.
+* ``rope_append(q, k, v, cos, sin, key_cache, value_cache, write_index)``
+  -- the graph step's RoPE + ``index_copy_`` append (SE:927-932).
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+
+HEAD_DIM = 64
+MAX_GROUPS = 16
+# MI355X: 256 compute units in 8 XCDs.
+NUM_CUS = 256
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _require_cuda_fp16(name: str, t: torch.Tensor, ndim: int | None = None) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a tensor")
+    if t.device.type != "cuda":
+        raise RuntimeError(f"{name} must be a HIP device tensor (got {t.device}); there is no CPU path")
+    if t.dtype != torch.float16:
+        raise TypeError(f"{name} must be float16 (got {t.dtype})")
+    if ndim is not None and t.dim() != ndim:
+        raise ValueError(f"{name} must be {ndim}-D (got shape {tuple(t.shape)})")
+    if t.shape[-1] != HEAD_DIM or t.stride(-1) != 1:
+        raise ValueError(f"{name}: last dim must be {HEAD_DIM} with stride 1 (shape {tuple(t.shape)}, "
+                         f"stride {t.stride()})")
+
+
+# --------------------------------------------------------------------------
+# decode
+# --------------------------------------------------------------------------
+
+def choose_splits(batch: int, kv_heads: int, length: int, min_keys: int = 64,
+                  target_workgroups: int = NUM_CUS) -> int:
+    """Split count for the decode kernel on MI355X.
+
+    About one (split, b, kv-head) workgroup per CU -- measured best from 2.5 MB
+    to 67 MB of K/V -- and never splits shorter than ``min_keys`` slots.  (The
+    reference's rule, ``max(1, min(32, 272 // (B*KVH), cap // 256))`` at
+    SE:1027, targets 68 SMs.)
+    """
+    by_len = max(1, math.ceil(length / min_keys))
+    by_cus = max(1, math.ceil(target_workgroups / max(1, batch * kv_heads)))
+    return max(1, min(by_len, by_cus, 1024))
+
+
+def prefer_fused(splits: int) -> bool:
+    """Single-launch merge pays off for few splits; above that the second
+    (combine) launch is cheaper than cross-XCD write-through traffic."""
+    return 1 < splits <= 8
+
+
+def make_flash_scratch(batch: int, kv_heads: int, groups: int, capacity: int,
+                       device, splits: int | None = None, fused: bool | None = None,
+                       head_dim: int = HEAD_DIM):
+    """Static scratch for ``flash_decode_attention`` (cf. SE:1028-1045).
+
+    Returns ``(acc, m, l, out)`` -- the reference's tuple -- plus a zeroed
+    int32 ``ticket`` (``ticket_size`` counters) when ``fused`` (single-launch
+    merge; default ``prefer_fused(splits)``).  All addresses stay fixed, so
+    the tuple can be captured into a hipGraph.
+    """
+    splits = choose_splits(batch, kv_heads, capacity) if splits is None else splits
+    fused = prefer_fused(splits) if fused is None else fused
+    f32 = dict(device=device, dtype=torch.float32)
+    acc = torch.zeros(batch, kv_heads, splits, groups, head_dim, **f32)
+    m = torch.zeros(batch, kv_heads, splits, groups, **f32)
+    l = torch.zeros(batch, kv_heads, splits, groups, **f32)
+    out = torch.zeros(batch, kv_heads, groups, head_dim, device=device, dtype=torch.float16)
+    if not fused:
+        return acc, m, l, out
+    ticket = torch.zeros(ticket_size(batch, kv_heads, splits), device=device, dtype=torch.int32)
+    return acc, m, l, out, ticket
+
+
+def ticket_size(batch: int, kv_heads: int, splits: int) -> int:
+    """int32 counters the single-launch merge needs: one per 16-split group plus one, per (b, h)."""
+    return batch * kv_heads * ((splits + 15) // 16 + 1)
+
+
+def flash_decode_attention(grouped: torch.Tensor, key_cache: torch.Tensor,
+                           value_cache: torch.Tensor, attn_bias: torch.Tensor | None,
+                           flash, kv_last: torch.Tensor | None = None,
+                           scale: float | None = None) -> torch.Tensor:
+    """Drop-in for ``StudentEngine._flash_decode_attention`` (SE:834-874).
+
+    grouped (B, KVH, G, D) fp16; key_cache/value_cache (B, KVH, cap, D) fp16;
+    attn_bias (B, cap) fp16 additive bias or None; ``flash`` is the
+    reference's ``(acc, m, l, out)`` static scratch -- the split count is
+    ``acc.shape[2]`` as in the reference -- optionally followed by an int32
+    ``ticket`` (see ``make_flash_scratch``) that selects the single-launch
+    merge.  ``kv_last`` (optional, device int64, shape (1,) or (B,)) is the
+    last slot that can be valid; slots after it are skipped (the engine passes
+    its ``write_index``).  Writes and returns ``out``.
+    """
+    acc, m, l, out = flash[:4]
+    ticket = flash[4] if len(flash) > 4 else None
+    _require_cuda_fp16("grouped", grouped, 4)
+    _require_cuda_fp16("key_cache", key_cache, 4)
+    _require_cuda_fp16("value_cache", value_cache, 4)
+    _require_cuda_fp16("out", out, 4)
+    b, kvh, g, d = grouped.shape
+    cap = key_cache.shape[2]
+    if key_cache.shape[:2] != (b, kvh) or value_cache.shape != key_cache.shape:
+        raise ValueError(f"cache shape {tuple(key_cache.shape)} / {tuple(value_cache.shape)} "
+                         f"does not match grouped {tuple(grouped.shape)}")
+    splits = acc.shape[2]
+    if acc.shape != (b, kvh, splits, g, d) or m.shape != (b, kvh, splits, g) or l.shape != m.shape:
+        raise ValueError("flash scratch shapes do not match (B, KVH, S, G, D) / (B, KVH, S, G)")
+    for name, t in (("acc", acc), ("m", m), ("l", l)):
+        if t.dtype != torch.float32 or not t.is_contiguous() or t.device != grouped.device:
+            raise ValueError(f"flash scratch {name} must be contiguous fp32 on {grouped.device}")
+    if out.shape != (b, kvh, g, d):
+        raise ValueError(f"out must be {(b, kvh, g, d)}")
+    if attn_bias is not None:
+        if attn_bias.dtype != torch.float16 or attn_bias.device != grouped.device:
+            raise TypeError("attn_bias must be fp16 on the same device")
+        if attn_bias.dim() != 2 or attn_bias.shape != (b, cap) or attn_bias.stride(1) != 1:
+            raise ValueError(f"attn_bias must be (B, cap) = {(b, cap)} with unit last stride")
+    if ticket is not None:
+        need = ticket_size(b, kvh, splits)
+        if ticket.dtype != torch.int32 or ticket.numel() < need or not ticket.is_contiguous():
+            raise ValueError(f"ticket must be a contiguous int32 tensor with {need} elements")
+    kv_last_sb = 0
+    if kv_last is not None:
+        if kv_last.dtype != torch.int64 or kv_last.device != grouped.device:
+            raise TypeError("kv_last must be an int64 device tensor")
+        if kv_last.numel() == 1:
+            kv_last_sb = 0
+        elif kv_last.numel() == b and kv_last.dim() == 1:
+            kv_last_sb = kv_last.stride(0)
+        else:
+            raise ValueError("kv_last must hold 1 or B elements")
+    scale = d ** -0.5 if scale is None else scale
+    lib = _lib.load()
+    with torch.cuda.device(grouped.device):
+        rc = lib.qf_decode_attn(
+            grouped.data_ptr(), grouped.stride(0), grouped.stride(1), grouped.stride(2),
+            key_cache.data_ptr(), key_cache.stride(0), key_cache.stride(1), key_cache.stride(2),
+            value_cache.data_ptr(), value_cache.stride(0), value_cache.stride(1), value_cache.stride(2),
+            _ptr(attn_bias), 0 if attn_bias is None else attn_bias.stride(0),
+            _ptr(kv_last), kv_last_sb,
+            acc.data_ptr(), m.data_ptr(), l.data_ptr(), splits,
+            _ptr(ticket),
+            out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
+            b, kvh, g, d, cap, float(scale), _stream(grouped.device))
+    _lib.check(rc, "qf_decode_attn")
+    return out
+
+
+def decode_attention(grouped, key_cache, value_cache, attn_bias=None, splits=None,
+                     kv_last=None, fused=None):
+    """Convenience wrapper: allocates scratch and runs ``flash_decode_attention``."""
+    b, kvh, g, _ = grouped.shape
+    flash = make_flash_scratch(b, kvh, g, key_cache.shape[2], grouped.device, splits, fused)
+    return flash_decode_attention(grouped, key_cache, value_cache, attn_bias, flash, kv_last)
+
+
+# --------------------------------------------------------------------------
+# decode RoPE + append
+# --------------------------------------------------------------------------
+
+def _as_rows(name: str, t: torch.Tensor, batch: int) -> torch.Tensor:
+    """View a per-row table ((B, D), (B, 1, D) or (B, 1, 1, D)) as (B, D)."""
+    if t.numel() != batch * HEAD_DIM:
+        raise ValueError(f"{name} must hold B*D = {batch * HEAD_DIM} values (shape {tuple(t.shape)})")
+    return t.reshape(batch, HEAD_DIM)
+
+
+def rope_append(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                cos: torch.Tensor, sin: torch.Tensor, key_cache: torch.Tensor,
+                value_cache: torch.Tensor, write_index: torch.Tensor,
+                out: torch.Tensor | None = None) -> torch.Tensor:
+    """RoPE + KV-cache append of the graph decode step (SE:927-932).
+
+    query (B, QH, 1, D), key/value (B, KVH, 1, D) -- the transposed views of
+    the fused QKV projection; cos/sin the per-step fp16 tables (B, 1, 1, D)
+    (SE:912-915, any shape holding B*D values); caches (B, KVH, cap, D);
+    write_index a one-element int64 device tensor.  Writes
+    ``key_cache[:, :, slot] = rope(key)`` and ``value_cache[:, :, slot] =
+    value`` with ``slot = write_index[0]`` read on the device, and returns
+    ``rope(query)`` (a new (B, QH, 1, D) tensor, or ``out``).
+    """
+    for n, t in (("query", query), ("key", key), ("value", value),
+                 ("key_cache", key_cache), ("value_cache", value_cache)):
+        _require_cuda_fp16(n, t, 4)
+    b, qh, tq, d = query.shape
+    kvh = key.shape[1]
+    if tq != 1 or key.shape != (b, kvh, 1, d) or value.shape != key.shape:
+        raise ValueError("rope_append expects one token: query (B, QH, 1, D), key/value (B, KVH, 1, D)")
+    if key_cache.shape[:2] != (b, kvh) or value_cache.shape != key_cache.shape:
+        raise ValueError("cache shape does not match key")
+    if write_index.dtype != torch.int64 or write_index.device != query.device:
+        raise TypeError("write_index must be an int64 device tensor")
+    cos2 = _as_rows("cos", cos, b)
+    sin2 = _as_rows("sin", sin, b)
+    for n, t in (("cos", cos2), ("sin", sin2)):
+        if t.dtype != torch.float16 or t.device != query.device or t.stride(1) != 1:
+            raise ValueError(f"{n} must be fp16 on the query's device with unit last stride")
+    if cos2.stride(0) != sin2.stride(0):
+        cos2, sin2 = cos2.contiguous(), sin2.contiguous()
+    if out is None:
+        out = torch.empty((b, qh, 1, d), device=query.device, dtype=query.dtype)
+    lib = _lib.load()
+    with torch.cuda.device(query.device):
+        rc = lib.qf_rope_append(
+            query.data_ptr(), query.stride(0), query.stride(1),
+            key.data_ptr(), key.stride(0), key.stride(1),
+            value.data_ptr(), value.stride(0), value.stride(1),
+            cos2.data_ptr(), sin2.data_ptr(), cos2.stride(0),
+            key_cache.data_ptr(), key_cache.stride(0), key_cache.stride(1), key_cache.stride(2),
+            value_cache.data_ptr(), value_cache.stride(0), value_cache.stride(1), value_cache.stride(2),
+            write_index.data_ptr(),
+            out.data_ptr(), out.stride(0), out.stride(1),
+            b, qh, kvh, d, key_cache.shape[2], _stream(query.device))
+    _lib.check(rc, "qf_rope_append")
+    return out
+
+
+# --------------------------------------------------------------------------
+# prefill
+# --------------------------------------------------------------------------
+
+def _prefill_launch(query, key, value, out, cos=None, sin=None, key_cache=None,
+                    value_cache=None, start_pos=0):
+    for n, t in (("query", query), ("key", key), ("value", value), ("out", out)):
+        _require_cuda_fp16(n, t, 4)
+    b, qh, s, d = query.shape
+    kvh = key.shape[1]
+    if key.shape != (b, kvh, s, d) or value.shape != key.shape or qh % kvh != 0:
+        raise ValueError(f"prefill shapes: query {tuple(query.shape)}, key {tuple(key.shape)}, "
+                         f"value {tuple(value.shape)}")
+    cs_sb = cs_sn = 0
+    if cos is not None or sin is not None:
+        if cos is None or sin is None:
+            raise ValueError("cos and sin go together")
+        # Accept (S, D), (B, S, D) or the engine's (B, 1, S, D).
+        def table(n, t):
+            _require_cuda_fp16(n, t)
+            if t.dim() == 4:
+                t = t.squeeze(1)
+            if t.dim() == 2:
+                t = t.unsqueeze(0)
+            if t.dim() != 3 or t.shape[1] != s or t.shape[0] not in (1, b):
+                raise ValueError(f"{n} must be (S, D), (B, S, D) or (B, 1, S, D) for S={s}")
+            return t
+        cos, sin = table("cos", cos), table("sin", sin)
+        if cos.stride() != sin.stride() or cos.shape != sin.shape:
+            cos, sin = cos.contiguous(), sin.contiguous()
+        cs_sb = 0 if cos.shape[0] == 1 else cos.stride(0)
+        cs_sn = cos.stride(1)
+    cap = 0
+    if key_cache is not None or value_cache is not None:
+        if key_cache is None or value_cache is None:
+            raise ValueError("key_cache and value_cache go together")
+        _require_cuda_fp16("key_cache", key_cache, 4)
+        _require_cuda_fp16("value_cache", value_cache, 4)
+        cap = key_cache.shape[2]
+        if key_cache.shape[:2] != (b, kvh) or value_cache.shape != key_cache.shape:
+            raise ValueError("cache shape does not match key")
+        if start_pos < 0 or start_pos + s > cap:
+            raise ValueError(f"start_pos {start_pos} + S {s} exceeds cache capacity {cap}")
+    kc_s = key_cache.stride()[:3] if key_cache is not None else (0, 0, 0)
+    vc_s = value_cache.stride()[:3] if value_cache is not None else (0, 0, 0)
+    lib = _lib.load()
+    with torch.cuda.device(query.device):
+        rc = lib.qf_prefill_attn(
+            query.data_ptr(), *query.stride()[:3],
+            key.data_ptr(), *key.stride()[:3],
+            value.data_ptr(), *value.stride()[:3],
+            _ptr(cos), _ptr(sin), cs_sb, cs_sn,
+            _ptr(key_cache), *kc_s,
+            _ptr(value_cache), *vc_s,
+            int(start_pos), cap,
+            out.data_ptr(), *out.stride()[:3],
+            b, qh, kvh, s, d, float(d ** -0.5), _stream(query.device))
+    _lib.check(rc, "qf_prefill_attn")
+    return out
+
+
+@torch.library.custom_op("student_qwen::gqa_flash_prefill", mutates_args=())
+def gqa_flash_prefill(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor) -> torch.Tensor:
+    """Causal GQA flash-prefill (SE:254-280): (B, QH, S, D) x (B, KVH, S, D)^2 -> (B, QH, S, D)."""
+    out = torch.empty(query.shape, device=query.device, dtype=query.dtype)
+    return _prefill_launch(query, key, value, out)
+
+
+@gqa_flash_prefill.register_fake
+def _gqa_flash_prefill_fake(query, key, value):
+    return torch.empty(query.shape, device=query.device, dtype=query.dtype)
+
+
+@torch.library.custom_op("student_qwen::gqa_flash_prefill_rope_append",
+                         mutates_args=("key_cache", "value_cache"))
+def gqa_flash_prefill_rope_append(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                                  cos: torch.Tensor, sin: torch.Tensor,
+                                  key_cache: torch.Tensor, value_cache: torch.Tensor,
+                                  start_pos: int) -> torch.Tensor:
+    """Causal prefill on pre-RoPE q/k with RoPE and the cache append fused.
+
+    Rotates q and k with the fp16 tables ``cos``/``sin`` ((S, D), (B, S, D) or
+    (B, 1, S, D); SE:545-548), attends causally, writes the rotated k and the
+    raw v to ``cache[:, :, start_pos:start_pos+S]`` (SE:715-716) and returns
+    the attention output (B, QH, S, D).
+    """
+    out = torch.empty(query.shape, device=query.device, dtype=query.dtype)
+    return _prefill_launch(query, key, value, out, cos, sin, key_cache, value_cache, start_pos)
+
+
+@gqa_flash_prefill_rope_append.register_fake
+def _gqa_flash_prefill_rope_append_fake(query, key, value, cos, sin, key_cache, value_cache,
+                                        start_pos):
+    return torch.empty(query.shape, device=query.device, dtype=query.dtype)

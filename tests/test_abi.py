@@ -1,0 +1,103 @@
+"""The C-ABI library loads and exports every entry point the header declares.
+
+Runs without a GPU: only argument rejections (which return before any HIP
+call) are exercised.
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from qwenforge_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "qf_attn.h"
+
+
+def _declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+char\*|int)\s+(qf_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_three_kernels():
+    names = _declared()
+    for n in ("qf_decode_attn", "qf_prefill_attn", "qf_rope_append", "qf_error_string",
+              "qf_abi_version"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in _declared():
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_version_and_error_strings():
+    lib = _lib.load()
+    assert lib.qf_abi_version() == 100
+    assert lib.qf_error_string(0) == b"success"
+    assert b"invalid" in lib.qf_error_string(-1)
+    assert b"unsupported" in lib.qf_error_string(-2)
+
+
+def _decode_call(lib, **over):
+    args = dict(q=16, k=16, v=16, acc=16, m=16, l=16, out=16, splits=1, B=1, KVH=2, G=7, D=64, cap=8)
+    args.update(over)
+    a = args
+    return lib.qf_decode_attn(a["q"], 0, 0, 0, a["k"], 0, 0, 0, a["v"], 0, 0, 0, None, 0, None, 0,
+                              a["acc"], a["m"], a["l"], a["splits"], None, a["out"], 0, 0, 0,
+                              a["B"], a["KVH"], a["G"], a["D"], a["cap"], 0.125, None)
+
+
+def test_decode_rejects_bad_arguments_without_launching():
+    lib = _lib.load()
+    assert _decode_call(lib, D=128) == -2
+    assert _decode_call(lib, G=17) == -2
+    assert _decode_call(lib, G=0) == -2
+    assert _decode_call(lib, q=None) == -1
+    assert _decode_call(lib, splits=0) == -1
+    assert _decode_call(lib, cap=0) == -1
+    assert _decode_call(lib, q=18) == -1  # misaligned pointer
+
+
+def test_prefill_and_append_reject_bad_arguments():
+    lib = _lib.load()
+    rc = lib.qf_prefill_attn(16, 0, 0, 0, 16, 0, 0, 0, 16, 0, 0, 0, None, None, 0, 0,
+                             None, 0, 0, 0, None, 0, 0, 0, 0, 0, 16, 0, 0, 0,
+                             1, 14, 2, 8, 32, 0.125, None)
+    assert rc == -2
+    rc = lib.qf_prefill_attn(16, 0, 0, 0, 16, 0, 0, 0, 16, 0, 0, 0, 16, None, 0, 0,
+                             None, 0, 0, 0, None, 0, 0, 0, 0, 0, 16, 0, 0, 0,
+                             1, 14, 2, 8, 64, 0.125, None)
+    assert rc == -1  # cos without sin
+    rc = lib.qf_prefill_attn(16, 0, 0, 0, 16, 0, 0, 0, 16, 0, 0, 0, None, None, 0, 0,
+                             16, 0, 0, 0, 16, 0, 0, 0, 5, 8, 16, 0, 0, 0,
+                             1, 14, 2, 8, 64, 0.125, None)
+    assert rc == -1  # start_pos + S > cap
+    rc = lib.qf_rope_append(16, 0, 0, 16, 0, 0, 16, 0, 0, 16, 16, 0, 16, 0, 0, 0, 16, 0, 0, 0,
+                            None, 16, 0, 0, 1, 14, 2, 64, 8, None)
+    assert rc == -1  # no write_index
+
+
+def test_ops_refuse_cpu_tensors():
+    torch = pytest.importorskip("torch")
+    from qwenforge_amd import ops
+
+    q = torch.zeros(1, 2, 7, 64, dtype=torch.float16)
+    k = torch.zeros(1, 2, 16, 64, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        ops.decode_attention(q, k, k)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        torch.ops.student_qwen.gqa_flash_prefill(torch.zeros(1, 14, 8, 64, dtype=torch.float16),
+                                                 torch.zeros(1, 2, 8, 64, dtype=torch.float16),
+                                                 torch.zeros(1, 2, 8, 64, dtype=torch.float16))
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "absent.so")
+    with pytest.raises(RuntimeError, match="missing"):
+        _lib.load()
+    assert ctypes  # keeps the import used

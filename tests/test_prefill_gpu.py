@@ -1,0 +1,93 @@
+"""Parity of the HIP causal flash-prefill (+ fused RoPE and cache append).
+
+Oracle: ``oracle.causal_prefill`` (SE:164-251 semantics, fp32) on inputs
+rotated by ``oracle.apply_rope_fp16`` (the eager fp16 sequence, SE:927-928).
+Attention tolerance 2e-3 max-abs-err; cache contents bit-exact.
+"""
+
+import pytest
+import torch
+
+import oracle
+from qwenforge_amd import ops, workloads
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+def _err(a, b):
+    return (a.float() - b.float()).abs().max().item()
+
+
+def test_config4_rope_append_s2048(dev):
+    case = workloads.prefill_case(2048, seed=0)
+    print("[prefill cfg4 S=2048]", flush=True)
+    c = case.to(dev)
+    kc = torch.zeros(1, 2, 2048, 64, dtype=torch.float16, device=dev)
+    vc = torch.zeros_like(kc)
+    out = torch.ops.student_qwen.gqa_flash_prefill_rope_append(c.query, c.key, c.value, c.cos, c.sin,
+                                                              kc, vc, 0)
+    torch.cuda.synchronize()
+    q_rot = oracle.apply_rope_fp16(case.query, case.cos, case.sin)
+    k_rot = oracle.apply_rope_fp16(case.key, case.cos, case.sin)
+    ref = oracle.causal_prefill(q_rot, k_rot, case.value)
+    assert _err(out.cpu(), ref) <= TOL
+    assert torch.equal(kc.cpu(), k_rot)
+    assert torch.equal(vc.cpu(), case.value)
+
+
+@pytest.mark.parametrize("seq", [1, 17, 64, 100, 513])
+@pytest.mark.parametrize("batch", [1, 2])
+def test_plain_prefill_ragged_lengths(dev, seq, batch):
+    case = workloads.prefill_case(seq, batch=batch, seed=seq + batch)
+    c = case.to(dev)
+    out = torch.ops.student_qwen.gqa_flash_prefill(c.query, c.key, c.value)
+    torch.cuda.synchronize()
+    ref = oracle.causal_prefill(case.query, case.key, case.value)
+    assert _err(out.cpu(), ref) <= TOL
+
+
+def test_projection_views_with_distinct_v_strides(dev):
+    """q/k/v as views of one fused projection (SE:754-766): V's strides differ from K's."""
+    gen = torch.Generator("cpu").manual_seed(3)
+    b, s = 2, 300
+    projected = torch.randn(b, s, 1152, generator=gen).half()
+    q, k, v = projected.split((896, 128, 128), dim=-1)
+    q = q.view(b, s, 14, 64).transpose(1, 2)
+    k = k.view(b, s, 2, 64).transpose(1, 2)
+    v = v.view(b, s, 2, 64).transpose(1, 2)
+    pg = projected.to(dev)
+    qg, kg, vg = pg.split((896, 128, 128), dim=-1)
+    qg = qg.view(b, s, 14, 64).transpose(1, 2)
+    kg = kg.view(b, s, 2, 64).transpose(1, 2)
+    vg = vg.view(b, s, 2, 64).transpose(1, 2)
+    out = torch.ops.student_qwen.gqa_flash_prefill(qg, kg, vg)
+    torch.cuda.synchronize()
+    ref = oracle.causal_prefill(q, k, v)
+    assert _err(out.cpu(), ref) <= TOL
+
+
+def test_append_at_offset_leaves_other_slots(dev):
+    case = workloads.prefill_case(130, batch=2, seed=9)
+    c = case.to(dev)
+    kc = torch.full((2, 2, 400, 64), 3.0, dtype=torch.float16, device=dev)
+    vc = torch.full_like(kc, -2.0)
+    start = 77
+    out = ops.gqa_flash_prefill_rope_append(c.query, c.key, c.value, c.cos, c.sin, kc, vc, start)
+    torch.cuda.synchronize()
+    k_rot = oracle.apply_rope_fp16(case.key, case.cos, case.sin)
+    kcc, vcc = kc.cpu(), vc.cpu()
+    assert torch.equal(kcc[:, :, start:start + 130], k_rot)
+    assert torch.equal(vcc[:, :, start:start + 130], case.value)
+    assert bool((kcc[:, :, :start] == 3.0).all()) and bool((kcc[:, :, start + 130:] == 3.0).all())
+    assert bool((vcc[:, :, :start] == -2.0).all()) and bool((vcc[:, :, start + 130:] == -2.0).all())
+    q_rot = oracle.apply_rope_fp16(case.query, case.cos, case.sin)
+    assert _err(out.cpu(), oracle.causal_prefill(q_rot, k_rot, case.value)) <= TOL
+
+
+def test_first_row_is_first_value(dev):
+    case = workloads.prefill_case(200, seed=4)
+    c = case.to(dev)
+    out = ops.gqa_flash_prefill(c.query, c.key, c.value).cpu()
+    expect = case.value.repeat_interleave(7, dim=1)[:, :, 0]
+    assert _err(out[:, :, 0], expect) == 0.0
