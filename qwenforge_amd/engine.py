@@ -1,0 +1,204 @@
+"""Greedy Qwen2-shaped decode engine around the HIP attention kernels.
+
+Mirrors the reference's cached generation path without the tokenizer:
+
+* ``prefill`` -- ``StudentEngine._prefill`` (SE:679-737): per layer RMSNorm,
+  fused QKV projection, then ONE fused HIP launch does rotate-half RoPE, the
+  causal GQA attention and the KV-cache append (it replaces the eager RoPE
+  SE:698-699/556-577, the slice append SE:715-716 and SDPA SE:719-725);
+  o_proj, MLP, last-token logits.
+* ``decode`` -- ``_decode_tokens_graphed`` (SE:984-1133) replaying a captured
+  ``_decode_step_static`` (SE:876-982): per layer RMSNorm, QKV, the HIP
+  RoPE+append kernel (SE:927-932), the HIP split-K decode attention bounded by
+  the device-side write slot (SE:941-943), o_proj, MLP; final norm, lm_head,
+  argmax.  The per-step bookkeeping the reference does on the host between
+  replays (bias slot, write slot, positions, token store; SE:1126-1132) runs
+  inside the graph as device ops, so a step is a single graph replay.
+
+GEMMs, RMSNorm and SwiGLU stay torch ops (hipBLASLt / ATen kernels), as in the
+reference.  Everything is fp16 storage with the reference's op order.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from . import ops
+from .model import Qwen2Config
+from .rope import cos_sin, inv_freq
+
+
+class DecodeEngine:
+    """Batched greedy decoding of a Qwen2-shaped model on one MI355X."""
+
+    def __init__(self, cfg: Qwen2Config, weights: dict, device="cuda"):
+        self.cfg = cfg
+        self.device = torch.device(device)
+        self.w = weights
+        self.inv_freq = inv_freq(cfg.head_dim, cfg.rope_theta, self.device)
+        self.scale = cfg.head_dim ** -0.5
+        self._ctx = None
+
+    # ------------------------------------------------------------------ helpers
+    def _rms(self, x, weight):
+        return F.rms_norm(x, (self.cfg.hidden,), weight, self.cfg.rms_eps)
+
+    def _mlp(self, x, layer):
+        gate, up = F.linear(x, layer["gate_up_weight"]).chunk(2, dim=-1)
+        return F.linear(F.silu(gate) * up, layer["down_weight"])
+
+    def _qkv(self, x, layer):
+        cfg = self.cfg
+        b, t, _ = x.shape
+        projected = F.linear(x, layer["qkv_weight"], layer["qkv_bias"])
+        q, k, v = projected.split((cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim,
+                                   cfg.kv_heads * cfg.head_dim), dim=-1)
+        q = q.view(b, t, cfg.heads, cfg.head_dim).transpose(1, 2)
+        k = k.view(b, t, cfg.kv_heads, cfg.head_dim).transpose(1, 2)
+        v = v.view(b, t, cfg.kv_heads, cfg.head_dim).transpose(1, 2)
+        return q, k, v
+
+    # ------------------------------------------------------------------ prefill
+    def new_caches(self, batch: int, capacity: int):
+        """Zero-initialised (B, KVH, cap, D) caches, one pair per layer (SE:705-714)."""
+        cfg = self.cfg
+        shape = (batch, cfg.kv_heads, capacity, cfg.head_dim)
+        return [(torch.zeros(shape, device=self.device, dtype=torch.float16),
+                 torch.zeros(shape, device=self.device, dtype=torch.float16))
+                for _ in range(cfg.layers)]
+
+    @torch.no_grad()
+    def prefill(self, input_ids: torch.Tensor, caches):
+        """Equal-length prompts (B, S) -> last-token logits (B, vocab); fills the caches."""
+        cfg = self.cfg
+        b, s = input_ids.shape
+        hidden = F.embedding(input_ids, self.w["embed"])
+        cos, sin = cos_sin(torch.arange(s, device=self.device), self.inv_freq)
+        for layer, (kc, vc) in zip(self.w["layers"], caches):
+            residual = hidden
+            q, k, v = self._qkv(self._rms(hidden, layer["input_norm"]), layer)
+            att = ops.gqa_flash_prefill_rope_append(q, k, v, cos, sin, kc, vc, 0)
+            att = att.transpose(1, 2).reshape(b, s, cfg.hidden)
+            hidden = residual + F.linear(att, layer["o_weight"])
+            residual = hidden
+            hidden = residual + self._mlp(self._rms(hidden, layer["post_norm"]), layer)
+        last = self._rms(hidden[:, -1], self.w["final_norm"])
+        return F.linear(last, self.w["lm_head"])
+
+    # ------------------------------------------------------------------ decode
+    def _step(self, ctx):
+        """One static-shape decode step (the captured graph body)."""
+        cfg = self.cfg
+        b = ctx["token"].shape[0]
+        if ctx["bias"] is not None:
+            # The slot written by this step becomes valid (SE:1127).
+            ctx["bias"].index_fill_(1, ctx["write"], 0.0)
+        hidden = F.embedding(ctx["token"], self.w["embed"]).view(b, 1, cfg.hidden)
+        cos, sin = cos_sin(ctx["pos"], self.inv_freq)          # (B, D), once per step (SE:910-915)
+        for layer, (kc, vc) in zip(self.w["layers"], ctx["caches"]):
+            residual = hidden
+            q, k, v = self._qkv(self._rms(hidden, layer["input_norm"]), layer)
+            q_rot = ops.rope_append(q, k, v, cos, sin, kc, vc, ctx["write"])
+            grouped = q_rot.view(b, cfg.kv_heads, cfg.groups, cfg.head_dim)
+            att = ops.flash_decode_attention(grouped, kc, vc, ctx["bias"], ctx["flash"],
+                                             kv_last=ctx["write"], scale=self.scale)
+            hidden = residual + F.linear(att.reshape(b, 1, cfg.hidden), layer["o_weight"])
+            residual = hidden
+            hidden = residual + self._mlp(self._rms(hidden, layer["post_norm"]), layer)
+        hidden = self._rms(hidden, self.w["final_norm"]).squeeze(1)
+        logits = F.linear(hidden, self.w["lm_head"])
+        nxt = torch.argmax(logits, dim=-1)
+        ctx["logits"].copy_(logits)
+        ctx["token"].copy_(nxt)
+        ctx["rows"].index_copy_(1, ctx["step"], nxt.unsqueeze(1))
+        ctx["write"].add_(1)
+        ctx["pos"].add_(1)
+        ctx["step"].add_(1)
+
+    def make_context(self, caches, batch: int, max_new_tokens: int, bias_mask=None):
+        """Static buffers of the graph step.  ``bias_mask`` (B, cap) bool marks
+        valid prompt slots when rows are right-padded; None means no holes, so
+        the write-slot bound alone selects the valid keys and no bias is read."""
+        cfg = self.cfg
+        cap = caches[0][0].shape[2]
+        dev = self.device
+        bias = None
+        if bias_mask is not None:
+            bias = torch.full((batch, cap), torch.finfo(torch.float16).min, device=dev,
+                              dtype=torch.float16)
+            bias.masked_fill_(bias_mask, 0.0)
+        return {
+            "caches": caches,
+            "bias": bias,
+            "flash": ops.make_flash_scratch(batch, cfg.kv_heads, cfg.groups, cap, dev),
+            "token": torch.zeros(batch, device=dev, dtype=torch.long),
+            "pos": torch.zeros(batch, device=dev, dtype=torch.long),
+            "write": torch.zeros(1, device=dev, dtype=torch.long),
+            "step": torch.zeros(1, device=dev, dtype=torch.long),
+            "rows": torch.zeros(batch, max_new_tokens, device=dev, dtype=torch.long),
+            "logits": torch.zeros(batch, cfg.vocab, device=dev, dtype=torch.float16),
+        }
+
+    def capture(self, ctx):
+        """Capture ``_step`` into a hipGraph (2 warm-ups on a side stream, SE:1056-1074).
+
+        The warm-ups run with the write slot parked on the last cache slot, as
+        in the reference; the caller resets the state before replaying.
+        """
+        cap = ctx["caches"][0][0].shape[2]
+        side = torch.cuda.Stream(self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        saved = {k: ctx[k].clone() for k in ("token", "pos", "write", "step", "rows")}
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                ctx["write"].fill_(cap - 1)
+                ctx["step"].fill_(0)
+                self._step(ctx)
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            self._step(ctx)
+        for k, v in saved.items():
+            ctx[k].copy_(v)
+        if ctx["bias"] is not None:
+            ctx["bias"][:, cap - 1] = torch.finfo(torch.float16).min
+        torch.cuda.synchronize(self.device)
+        ctx["graph"] = graph
+        return graph
+
+    @torch.no_grad()
+    def generate(self, input_ids: torch.Tensor, max_new_tokens: int, timing: dict | None = None):
+        """Greedy ids (B, max_new_tokens) for equal-length prompts (B, S).
+
+        Capacity follows SE:1263-1273: prompt + new - 1, rounded up to 64.
+        ``timing`` (optional dict) receives prefill and decode times in ms
+        (HIP events on the current stream).
+        """
+        b, s = input_ids.shape
+        cap = (s + max(max_new_tokens - 1, 0) + 63) // 64 * 64
+        caches = self.new_caches(b, cap)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        ev[0].record()
+        logits = self.prefill(input_ids, caches)
+        first = torch.argmax(logits, dim=-1)
+        ev[1].record()
+        ctx = self.make_context(caches, b, max_new_tokens)
+        self.capture(ctx)
+        ctx["rows"][:, 0] = first
+        ctx["token"].copy_(first)
+        ctx["pos"].fill_(s)
+        ctx["write"].fill_(s)
+        ctx["step"].fill_(1)
+        torch.cuda.synchronize(self.device)
+        ev[2].record()
+        for _ in range(1, max_new_tokens):
+            ctx["graph"].replay()
+        ev[3].record()
+        torch.cuda.synchronize(self.device)
+        if timing is not None:
+            timing["prefill_ms"] = ev[0].elapsed_time(ev[1])
+            timing["decode_ms"] = ev[2].elapsed_time(ev[3])
+        self._ctx = ctx
+        return ctx["rows"].clone()

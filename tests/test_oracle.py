@@ -308,3 +308,20 @@ def test_oracle_catches_a_planted_transpose():
     assert (good - ref).abs().max().item() < 1e-12
     assert (bad - ref).abs().max().item() > 1e-2
     assert math.isfinite(good.abs().max().item())
+
+
+# ---------------------------------------------------------------- model step
+
+def test_model_decode_step_continues_prefill():
+    """Decoding token S over a prefilled cache reproduces prefill of S+1 tokens."""
+    import oracle.model as om
+    from qwenforge_amd.model import Qwen2Config, init_weights
+
+    cfg = Qwen2Config(layers=2, vocab=512, hidden=256, heads=4, kv_heads=2, head_dim=64,
+                      intermediate=256)
+    w = init_weights(cfg, "cpu", seed=3, std=0.1)
+    ids = torch.randint(0, cfg.vocab, (2, 12), generator=torch.Generator().manual_seed(4))
+    full, _ = om.prefill(w, cfg, ids, 64)
+    _, caches = om.prefill(w, cfg, ids[:, :11], 64)
+    step = om.decode_step(w, cfg, ids[:, 11], torch.full((2,), 11), caches, 11)
+    assert (full - step).abs().max().item() < 1e-4
