@@ -26,7 +26,10 @@ SOURCES = ["decode_attn.hip", "prefill_attn.hip", "rope_append.hip", "capi.cpp"]
 # Packed-fp32 VALU forms are disabled for all device code (they have produced
 # silently wrong results on this hardware pool); hipcc's host pass warns that it
 # does not know the feature, which is harmless.
-DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+                # MFMA results in VGPRs: the softmax reads every score tile and the
+                # accumulators are rescaled, so AGPR<->VGPR copies would dominate.
+                "-mllvm", "-amdgpu-mfma-vgpr-form"]
 COMMON_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", f"-I{ROOT / 'include'}"]
 
 

@@ -8,17 +8,25 @@
 //
 // One workgroup = 64 query rows of one query head (four wave64s x 16 rows);
 // query tiles are launched heaviest-first (the last rows see the most keys).
-// Per 64-key tile the workgroup cooperatively
+// K/V tiles of 64 keys are double-buffered in LDS: while the waves compute on
+// tile t, the registers already hold tile t+1's global loads, which are
+// rotated (K) and written to the other LDS buffer afterwards, so one barrier
+// per tile separates the phases and HBM latency overlaps the MFMA work.
+// Per 64-key tile the workgroup
 //   - loads K with 16-byte loads, applies RoPE in registers (both halves of a
 //     rotate-half pair are loaded by the same thread), stores the rotated rows
 //     to LDS in natural [key][d] layout,
-//   - loads V and stores it transposed ([d][key]) to LDS,
+//   - loads V four keys per thread and stores it transposed ([d][key]) with
+//     8-byte LDS writes,
 //   - on the diagonal tile of the group's first query head, also writes the
 //     rotated K and raw V into the cache (each key tile is written exactly
 //     once per (b, kv head)).
-// Each wave then computes S^T = K Q^T and O^T += V^T P^T with
-// v_mfma_f32_16x16x32_f16 and an online softmax in the log2 domain; Q is
-// rotated in registers once at the start.
+// Each wave computes S^T = K Q^T and O^T += V^T P^T with
+// v_mfma_f32_16x16x32_f16 and an online softmax in the log2 domain, one
+// max/rescale decision per 64-key tile (the output accumulators are only
+// rescaled when the running max grows by more than kRescaleSlack); Q is
+// rotated in registers once at the start.  The causal mask is applied only on
+// the diagonal and tail tiles.
 #include "qf_common.h"
 #include "../../include/qf_attn.h"
 
@@ -31,7 +39,7 @@ constexpr int kBM = 64;        // query rows per workgroup
 constexpr int kBN = 64;        // keys per tile
 constexpr int kWaves = 4;
 constexpr int kKStride = 72;   // LDS row stride (halves) of the K tile
-constexpr int kVtStride = 72;  // LDS row stride (halves) of the V^T tile
+constexpr int kVtStride = 68;  // LDS row stride (halves) of the V^T tile
 
 struct Args {
   const f16* q;
@@ -54,10 +62,124 @@ struct Args {
   float scale_log2;
 };
 
+// Registers holding one K/V tile between its global load and its LDS store.
+// The K rotation happens at store time, so the loads stay in flight while the
+// previous tile is computed.
+struct Stage {
+  f16x8 klo, khi;   // K row (tid >> 2), dims 8c..8c+7 and 32+8c..
+  f16x8 cs[4];      // cos/sin of that row for both halves (RoPE only)
+  f16x8 v[4];       // threads < 128: V rows 4m..4m+3, dims 8c'..8c'+7
+};
+
+// Loader mapping, fixed for the kernel: thread -> K row (tid >> 2) with the
+// 8-wide chunk pair 8*(tid & 3) / +32; threads < 128 -> V rows 4*(tid & 15)
+// .. +3 with dims 8*(tid >> 4) .. +7.  The per-thread pointers are computed
+// once; a tile only adds its uniform (scalar) row offset.
+struct Loader {
+  const f16* kp;     // K row pointer of tile 0 (+ chunk)
+  const f16* vp;     // first V row pointer of tile 0 (+ chunk)
+  int64_t cso;       // cos/sin element offset of tile 0's K row (+ chunk)
+  int krow, kc8, vrow, vc8;
+};
+
+template <bool kRope>
+__device__ __forceinline__ void stage_load(Stage& st, const Args& a, const f16* kb, const f16* vb,
+                                           int64_t cs_off, const Loader& ld, int key0, bool tail,
+                                           int tid) {
+  const int S = a.S;
+  if (!tail) {
+    const f16* kp = ld.kp + key0 * a.k_sn;
+    st.klo = load16(kp);
+    st.khi = load16(kp + 32);
+    if (kRope) {
+      const int64_t co = ld.cso + key0 * a.cs_sn;
+      st.cs[0] = load16(a.cos + co);
+      st.cs[1] = load16(a.sin + co);
+      st.cs[2] = load16(a.cos + co + 32);
+      st.cs[3] = load16(a.sin + co + 32);
+    }
+    if (tid < 128) {
+      const f16* vp = ld.vp + key0 * a.v_sn;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) st.v[r] = load16(vp + r * a.v_sn);
+    }
+    return;
+  }
+  // Last tile: rows past the sequence repeat row S-1 (their scores are masked).
+  {
+    int key = key0 + ld.krow;
+    key = key < S ? key : S - 1;
+    const f16* kp = kb + (int64_t)key * a.k_sn + ld.kc8;
+    st.klo = load16(kp);
+    st.khi = load16(kp + 32);
+    if (kRope) {
+      const int64_t co = cs_off + (int64_t)key * a.cs_sn + ld.kc8;
+      st.cs[0] = load16(a.cos + co);
+      st.cs[1] = load16(a.sin + co);
+      st.cs[2] = load16(a.cos + co + 32);
+      st.cs[3] = load16(a.sin + co + 32);
+    }
+  }
+  if (tid < 128) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      int key = key0 + ld.vrow + r;
+      key = key < S ? key : S - 1;
+      st.v[r] = load16(vb + (int64_t)key * a.v_sn + ld.vc8);
+    }
+  }
+}
+
+template <bool kRope>
+__device__ __forceinline__ void stage_rope(Stage& st) {
+  if (kRope) rope_pair(st.klo, st.khi, st.cs[0], st.cs[1], st.cs[2], st.cs[3]);
+}
+
+__device__ __forceinline__ void stage_store(const Stage& st, f16 (*ks)[kKStride],
+                                            f16 (*vts)[kVtStride], const Loader& ld, int tid) {
+  *reinterpret_cast<f16x8*>(&ks[ld.krow][ld.kc8]) = st.klo;
+  *reinterpret_cast<f16x8*>(&ks[ld.krow][32 + ld.kc8]) = st.khi;
+  if (tid < 128) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const f16x4 col4 = {st.v[0][e], st.v[1][e], st.v[2][e], st.v[3][e]};
+      *reinterpret_cast<f16x4*>(&vts[ld.vc8 + e][ld.vrow]) = col4;
+    }
+  }
+}
+
+// Rotated K and raw V of a tile into the cache at slots start_pos + key.
+__device__ __forceinline__ void stage_append(const Stage& st, const Args& a, int b, int hk,
+                                             const Loader& ld, int key0, int tid) {
+  const int S = a.S;
+  {
+    const int key = key0 + ld.krow;
+    if (key < S) {
+      f16* kd = a.kc + b * a.kc_sb + hk * a.kc_sh + (a.start_pos + key) * a.kc_sn;
+      store16(kd + ld.kc8, st.klo);
+      store16(kd + 32 + ld.kc8, st.khi);
+    }
+  }
+  if (tid < 128) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int key = key0 + ld.vrow + r;
+      if (key < S)
+        store16(a.vc + b * a.vc_sb + hk * a.vc_sh + (a.start_pos + key) * a.vc_sn + ld.vc8, st.v[r]);
+    }
+  }
+}
+
+// Running max is only moved when a tile's max exceeds it by more than this
+// many log2 units: until then p = exp2(s - m) <= 2^8 stays exact enough in
+// fp16 and the output accumulators need no rescaling (the final division by
+// the running sum makes the result independent of the reference point).
+constexpr float kRescaleSlack = 8.f;
+
 template <bool kRope, bool kAppend>
 __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(Args a) {
-  __shared__ __attribute__((aligned(16))) f16 ks[kBN][kKStride];
-  __shared__ __attribute__((aligned(16))) f16 vts[kD][kVtStride];
+  __shared__ __attribute__((aligned(16))) f16 ks[2][kBN][kKStride];
+  __shared__ __attribute__((aligned(16))) f16 vts[2][kD][kVtStride];
 
   const int n_mtiles = gridDim.x;
   const int mt = n_mtiles - 1 - blockIdx.x;  // heaviest tiles first
@@ -68,6 +190,25 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(Args a) {
   const int lane = tid & 63, w = tid >> 6;
   const int col = lane & 15, grp = lane >> 4;
   const int S = a.S;
+
+  const f16* kb = a.k + b * a.k_sb + hk * a.k_sh;
+  const f16* vb = a.v + b * a.v_sb + hk * a.v_sh;
+  const int64_t cs_off = b * a.cs_sb;  // this batch row's cos/sin tables
+  const bool writer = kAppend && (hq % a.G == 0);
+  const int key_end = (mt + 1) * kBM < S ? (mt + 1) * kBM : S;
+  const int n_ktiles = (key_end + kBN - 1) / kBN;
+  Loader ld;
+  ld.krow = tid >> 2;
+  ld.kc8 = 8 * (tid & 3);
+  ld.vrow = 4 * (tid & 15);
+  ld.vc8 = 8 * (tid >> 4);
+  ld.kp = kb + ld.krow * a.k_sn + ld.kc8;
+  ld.vp = vb + ld.vrow * a.v_sn + ld.vc8;
+  ld.cso = cs_off + ld.krow * a.cs_sn + ld.kc8;
+
+  // Tile 0 goes out first; Q is loaded and rotated while it is in flight.
+  Stage st;
+  stage_load<kRope>(st, a, kb, vb, cs_off, ld, 0, kBN > S, tid);
 
   // ---- Q^T operand (16 rows per wave), rotated in registers.
   const int qrow = mt * kBM + w * 16 + col;
@@ -84,97 +225,87 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(Args a) {
     }
   }
 
-  float m_run = kNegInf, l_run = 0.f;
+  float m_use = kNegInf, l_run = 0.f;
   f32x4 o[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const f16* kb = a.k + b * a.k_sb + hk * a.k_sh;
-  const f16* vb = a.v + b * a.v_sb + hk * a.v_sh;
-  const bool writer = kAppend && (hq % a.G == 0);
-  const int key_end = (mt + 1) * kBM < S ? (mt + 1) * kBM : S;
-  const int n_ktiles = (key_end + kBN - 1) / kBN;
+  stage_rope<kRope>(st);
+  if (writer && mt == 0) stage_append(st, a, b, hk, ld, 0, tid);
+  stage_store(st, ks[0], vts[0], ld, tid);
+  __syncthreads();
 
-  // Loader mapping: thread -> (key row, 8-wide chunk pair c / c+4 for K,
-  // 16-wide slice for V).
-  const int ld_key = tid >> 2, ld_c = tid & 3;
-
+  const float ks2 = a.scale_log2;
   for (int kt = 0; kt < n_ktiles; ++kt) {
+    const int buf = kt & 1;
     const int key0 = kt * kBN;
-    {
-      const int key = key0 + ld_key;
-      const int kc = key < S ? key : S - 1;
-      f16x8 klo = load16(kb + (int64_t)kc * a.k_sn + 8 * ld_c);
-      f16x8 khi = load16(kb + (int64_t)kc * a.k_sn + 32 + 8 * ld_c);
-      if (kRope) {
-        const int64_t co = b * a.cs_sb + (int64_t)kc * a.cs_sn + 8 * ld_c;
-        rope_pair(klo, khi, load16(a.cos + co), load16(a.sin + co), load16(a.cos + co + 32),
-                  load16(a.sin + co + 32));
-      }
-      *reinterpret_cast<f16x8*>(&ks[ld_key][8 * ld_c]) = klo;
-      *reinterpret_cast<f16x8*>(&ks[ld_key][32 + 8 * ld_c]) = khi;
-      const f16x8 v0 = load16(vb + (int64_t)kc * a.v_sn + 16 * ld_c);
-      const f16x8 v1 = load16(vb + (int64_t)kc * a.v_sn + 16 * ld_c + 8);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        vts[16 * ld_c + e][ld_key] = v0[e];
-        vts[16 * ld_c + 8 + e][ld_key] = v1[e];
-      }
-      if (writer && kt == mt && key < S) {
-        const int64_t slot = a.start_pos + key;
-        f16* kd = a.kc + b * a.kc_sb + hk * a.kc_sh + slot * a.kc_sn;
-        f16* vd = a.vc + b * a.vc_sb + hk * a.vc_sh + slot * a.vc_sn;
-        store16(kd + 8 * ld_c, klo);
-        store16(kd + 32 + 8 * ld_c, khi);
-        store16(vd + 16 * ld_c, v0);
-        store16(vd + 16 * ld_c + 8, v1);
-      }
-    }
-    __syncthreads();
+    const bool more = kt + 1 < n_ktiles;
+    if (more) stage_load<kRope>(st, a, kb, vb, cs_off, ld, key0 + kBN, key0 + 2 * kBN > S, tid);
 
-    // Two 32-key chunks per tile.
+    // S^T for the whole 64-key tile: block 2*ch + j holds keys
+    // key0 + 32*ch + 8*grp + 4*j + i in register i (column = query).
+    f32x4 c[4];
 #pragma unroll
-    for (int ch = 0; ch < 2; ++ch) {
-      f32x4 c[2];
+    for (int ch = 0; ch < 2; ++ch)
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const int krow = 32 * ch + 8 * (col >> 2) + 4 * j + (col & 3);
-        const f16x8 a0 = *reinterpret_cast<const f16x8*>(&ks[krow][8 * grp]);
-        const f16x8 a1 = *reinterpret_cast<const f16x8*>(&ks[krow][32 + 8 * grp]);
-        c[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-        c[j] = mfma16x16x32(a0, qf[0], c[j]);
-        c[j] = mfma16x16x32(a1, qf[1], c[j]);
+        const f16x8 a0 = *reinterpret_cast<const f16x8*>(&ks[buf][krow][8 * grp]);
+        const f16x8 a1 = *reinterpret_cast<const f16x8*>(&ks[buf][krow][32 + 8 * grp]);
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        acc = mfma16x16x32(a0, qf[0], acc);
+        c[2 * ch + j] = mfma16x16x32(a1, qf[1], acc);
       }
-      float sc[8];
-      const int kbase = key0 + 32 * ch + 8 * grp;
+    if (key0 + kBN > mt * kBM || key0 + kBN > S) {  // diagonal or tail tile: mask
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-        const int key = kbase + jj;
-        const float x = (jj < 4 ? c[0][jj] : c[1][jj - 4]) * a.scale_log2;
-        sc[jj] = (key <= qrow && key < S) ? x : kNegInf;
-      }
-      float mx = sc[0];
+      for (int blk = 0; blk < 4; ++blk)
 #pragma unroll
-      for (int jj = 1; jj < 8; ++jj) mx = fmaxf(mx, sc[jj]);
-      mx = col_max(mx);
-      const float m_new = fmaxf(m_run, mx);
-      const float safe_m = (m_new == kNegInf) ? 0.f : m_new;
-      const float resc = (m_new == kNegInf) ? 1.f : fast_exp2(m_run - m_new);
-      float psum = 0.f;
-      f16x8 pb;
+        for (int i = 0; i < 4; ++i) {
+          const int key = key0 + 32 * (blk >> 1) + 8 * grp + 4 * (blk & 1) + i;
+          if (!(key <= qrow && key < S)) c[blk][i] = kNegInf;
+        }
+    }
+    float mx = fmaxf(fmaxf(c[0][0], c[0][1]), fmaxf(c[0][2], c[0][3]));
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-        const float p = (sc[jj] == kNegInf) ? 0.f : fast_exp2(sc[jj] - safe_m);
+    for (int blk = 1; blk < 4; ++blk)
+      mx = fmaxf(mx, fmaxf(fmaxf(c[blk][0], c[blk][1]), fmaxf(c[blk][2], c[blk][3])));
+    mx *= ks2;
+    // The lane-local max decides (one ballot); the column max over the four
+    // lanes sharing a query is only formed on the rare rescale path, so every
+    // lane of a column keeps the same reference point.
+    if (__any(mx > m_use + kRescaleSlack)) {
+      const float m_new = fmaxf(m_use, col_max(mx));
+      const float resc = (m_new == kNegInf) ? 1.f : fast_exp2(m_use - m_new);
+      l_run *= resc;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) o[t] *= resc;
+      m_use = m_new;
+    }
+    const float neg_m = (m_use == kNegInf) ? 0.f : -m_use;
+    float psum = 0.f;
+    f16x8 pb[2];
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = fast_exp2(__builtin_fmaf(c[blk][i], ks2, neg_m));  // 0 for masked keys
         psum += p;
-        pb[jj] = (f16)p;
+        pb[blk >> 1][4 * (blk & 1) + i] = (f16)p;
       }
-      l_run = l_run * resc + psum;
-      m_run = m_new;
+    l_run += psum;
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch)
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const f16x8 va = *reinterpret_cast<const f16x8*>(&vts[16 * t + col][32 * ch + 8 * grp]);
-        o[t] = mfma16x16x32(va, pb, o[t] * resc);
+        const f16x4 va0 = *reinterpret_cast<const f16x4*>(&vts[buf][16 * t + col][32 * ch + 8 * grp]);
+        const f16x4 va1 = *reinterpret_cast<const f16x4*>(&vts[buf][16 * t + col][32 * ch + 8 * grp + 4]);
+        const f16x8 va = {va0[0], va0[1], va0[2], va0[3], va1[0], va1[1], va1[2], va1[3]};
+        o[t] = mfma16x16x32(va, pb[ch], o[t]);
       }
+    if (more) {
+      stage_rope<kRope>(st);
+      if (writer && kt + 1 == mt) stage_append(st, a, b, hk, ld, key0 + kBN, tid);
+      stage_store(st, ks[buf ^ 1], vts[buf ^ 1], ld, tid);
     }
     __syncthreads();
   }
