@@ -41,6 +41,8 @@ def _args():
     p.add_argument("--no-extras", action="store_true", help="headline line only")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--pmc-sample", action="store_true",
+                   help="run a short fixed kernel sequence for rocprofv3 --pmc and exit")
     return p.parse_args()
 
 
@@ -110,8 +112,26 @@ def bench_ragged_decode(steps, warmup, dev):
     graphs = [GraphStep(step_fn(cs)) for cs in sets]
     ms = _time_graphs(graphs, steps, warmup)
     step_bytes = sum(c.valid_bytes for c in layers)
+    fused = len(flash) > 4
+
+    # The dominant kernel alone: the split launch (qf_decode_split) over the
+    # same 24 layers, then the combine launch alone (unfused shape only).
+    def split_fn(cs):
+        def run():
+            for i, c in enumerate(cs):
+                ops.flash_decode_split(c.grouped, c.key_cache, c.value_cache, c.bias, flash[:4],
+                                       kv_last=kv_last[i])
+        return run
+
+    split_graphs = [GraphStep(split_fn(cs)) for cs in sets]
+    ms_split = _time_graphs(split_graphs, steps, warmup)
+    ms_combine = None
+    if not fused:
+        comb = GraphStep(lambda: [ops.flash_decode_combine(flash[:4]) for _ in layers])
+        ms_combine = _time_graphs([comb], steps, warmup)
     return dict(ms_per_step=ms, step_bytes=step_bytes, launches=len(layers), splits=splits,
-                replicas=replicas, layers=layers)
+                replicas=replicas, layers=layers, fused=fused, ms_split=ms_split,
+                ms_combine=ms_combine)
 
 
 def bench_long_decode(steps, warmup, dev):
@@ -190,6 +210,42 @@ def bench_e2e(dev, batches=(1, 4), prefix=1024, new_tokens=128):
     return out
 
 
+def pmc_sample(dev):
+    """A short fixed sequence for ``rocprofv3 --pmc`` passes (no timing):
+    a plain 64 MiB device copy (calibrates FETCH_SIZE / WRITE_SIZE against a
+    known byte count), then one config-2 step of split and combine launches."""
+    import torch
+
+    from qwenforge_amd import ops, workloads
+
+    src = torch.randn(32 << 20, device=dev, dtype=torch.float16)   # 64 MiB
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    layers = [c.to(dev) for c in workloads.decode_ragged_layers(24, 4, seed=0)]
+    cap_max = max(c.key_cache.shape[2] for c in layers)
+    flash = ops.make_flash_scratch(4, 2, 7, cap_max, dev, splits=ops.choose_splits(4, 2, cap_max),
+                                   fused=False)
+    for c in layers:
+        kv_last = torch.tensor([n - 1 for n in c.lengths], dtype=torch.int64, device=dev)
+        ops.flash_decode_split(c.grouped, c.key_cache, c.value_cache, c.bias, flash, kv_last=kv_last)
+        ops.flash_decode_combine(flash)
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_sample": "done", "copy_bytes": 2 * src.numel() * 2,
+                      "split_launches": len(layers),
+                      "split_bytes_mean": sum(c.valid_bytes for c in layers) / len(layers)}))
+
+
+def _traffic():
+    """HBM bytes per split launch measured with rocprofv3 counters (see profiles/)."""
+    path = os.path.join(ROOT, "profiles", "decode_split_cfg2_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f).get("traffic_bytes_per_launch")
+
+
 def cpu_baseline(layers, seconds):
     """The CPU oracle (fp32 restatement of SE:939-972) on config-2 layers, host cores."""
     import torch
@@ -231,12 +287,17 @@ def main():
     _lib.load()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.pmc_sample:
+        pmc_sample(dev)
+        return
 
     r = bench_ragged_decode(args.steps, args.warmup, dev)
     ms = r["ms_per_step"]
     gbs = r["step_bytes"] / (ms * 1e-3) / 1e9
     us_layer = ms * 1e3 / r["launches"]
     launch_bytes = r["step_bytes"] / r["launches"]
+    us_split = r["ms_split"] * 1e3 / r["launches"]
+    split_gbs = launch_bytes / (us_split * 1e-6) / 1e9
     line = {
         "metric": "flash-decode µs/layer + HBM GB/s (% of peak); decode tok/s at bs=1/4",
         "value": round(gbs, 2),
@@ -262,14 +323,17 @@ def main():
         "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
         "roofline": {
             "bound": "hbm",
-            "achieved": round(launch_bytes / (us_layer * 1e-6) / 1e9, 2),
+            "achieved": round(split_gbs, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(launch_bytes / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-            "traffic": None,
-            "kernel": "decode_split_kernel<true,true> (fused merge)",
+            "frac": round(split_gbs / HBM_PEAK_GBS, 4),
+            "traffic": _traffic(),
+            "kernel": "qf::decode_split_kernel<8, true, 1> (qf_decode_split, partial mode)",
             "bytes_per_launch": int(launch_bytes),
-            "avg_launch_us": round(us_layer, 3),
+            "avg_launch_us": round(us_split, 3),
+            "combine_kernel_avg_us": (None if r["ms_combine"] is None
+                                      else round(r["ms_combine"] * 1e3 / r["launches"], 3)),
+            "merge": "fused single launch" if r["fused"] else "split + combine launches",
         },
     }
     if not args.no_extras:

@@ -94,6 +94,26 @@ int qf_decode_attn(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sg,
                    void* stream);
 
 /*
+ * The two launches of the reference's decode, separately (SE:854-865 and
+ * SE:866-873): qf_decode_split writes the per-split partials (acc, m, l) with
+ * the contract of qf_decode_attn; qf_decode_combine merges `splits` partials
+ * of every (b, kv head) into `out`.  qf_decode_attn with ticket == NULL is
+ * exactly split followed by combine.
+ */
+int qf_decode_split(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sg,
+                    const void* k, int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                    const void* v, int64_t v_sb, int64_t v_sh, int64_t v_sn,
+                    const void* bias, int64_t bias_sb,
+                    const int64_t* kv_last, int64_t kv_last_sb,
+                    float* acc, float* m, float* l, int splits,
+                    int B, int KVH, int G, int D, int cap, float scale,
+                    void* stream);
+
+int qf_decode_combine(const float* acc, const float* m, const float* l, int splits,
+                      void* out, int64_t o_sb, int64_t o_sh, int64_t o_sg,
+                      int B, int KVH, int G, int D, void* stream);
+
+/*
  * Causal GQA flash-prefill.
  *
  * Replaces _gqa_flash_prefill_kernel (student_engine.py:164-251) as launched

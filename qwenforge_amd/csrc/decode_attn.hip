@@ -458,27 +458,32 @@ static int pick_waves(int splits, int B, int KVH) {
   return 4;
 }
 
-extern "C" int qf_decode_attn(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sg,
-                              const void* k, int64_t k_sb, int64_t k_sh, int64_t k_sn,
-                              const void* v, int64_t v_sb, int64_t v_sh, int64_t v_sn,
-                              const void* bias, int64_t bias_sb,
-                              const int64_t* kv_last, int64_t kv_last_sb,
-                              float* acc, float* m, float* l, int splits,
-                              int32_t* ticket,
-                              void* out, int64_t o_sb, int64_t o_sh, int64_t o_sg,
-                              int B, int KVH, int G, int D, int cap, float scale,
-                              void* stream) {
+// Validates the decode arguments and fills DecodeArgs; 0 or a QF_ERR_* code.
+static int make_args(DecodeArgs& a, const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sg,
+                     const void* k, int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                     const void* v, int64_t v_sb, int64_t v_sh, int64_t v_sn,
+                     const void* bias, int64_t bias_sb, const int64_t* kv_last,
+                     int64_t kv_last_sb, float* acc, float* m, float* l, int splits,
+                     int32_t* ticket, void* out, int64_t o_sb, int64_t o_sh, int64_t o_sg,
+                     int B, int KVH, int G, int D, int cap, float scale, bool need_qkv,
+                     bool need_out) {
   if (D != kD || G < 1 || G > kMaxG) return QF_ERR_UNSUPPORTED;
-  if (!q || !k || !v || !acc || !m || !l || !out) return QF_ERR_INVALID_ARG;
-  if (B < 1 || KVH < 1 || cap < 1 || splits < 1 || splits > 65535 || B * (int64_t)KVH > 65535)
+  if (!acc || !m || !l) return QF_ERR_INVALID_ARG;
+  if (B < 1 || KVH < 1 || splits < 1 || splits > 65535 || B * (int64_t)KVH > 65535)
     return QF_ERR_INVALID_ARG;
   if ((int64_t)B * KVH * G > 0x7fffffff) return QF_ERR_INVALID_ARG;
-  // 16-byte vector loads of q/k/v rows, 8-byte stores of out.
-  if (!aligned16(q) || !aligned16(k) || !aligned16(v)) return QF_ERR_INVALID_ARG;
-  if ((q_sb | q_sh | q_sg | k_sb | k_sh | k_sn | v_sb | v_sh | v_sn) & 7) return QF_ERR_INVALID_ARG;
-  if (((reinterpret_cast<uintptr_t>(out) & 7u) != 0) || ((o_sb | o_sh | o_sg) & 3)) return QF_ERR_INVALID_ARG;
-
-  DecodeArgs a;
+  if (!aligned16(acc)) return QF_ERR_INVALID_ARG;
+  if (need_qkv) {
+    if (!q || !k || !v || cap < 1) return QF_ERR_INVALID_ARG;
+    // 16-byte vector loads of q/k/v rows.
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v)) return QF_ERR_INVALID_ARG;
+    if ((q_sb | q_sh | q_sg | k_sb | k_sh | k_sn | v_sb | v_sh | v_sn) & 7) return QF_ERR_INVALID_ARG;
+  }
+  if (need_out) {
+    // 8-byte stores of out.
+    if (!out || (reinterpret_cast<uintptr_t>(out) & 7u) != 0 || ((o_sb | o_sh | o_sg) & 3))
+      return QF_ERR_INVALID_ARG;
+  }
   a.q = static_cast<const f16*>(q);
   a.q_sb = q_sb; a.q_sh = q_sh; a.q_sg = q_sg;
   a.k = static_cast<const f16*>(k);
@@ -496,14 +501,69 @@ extern "C" int qf_decode_attn(const void* q, int64_t q_sb, int64_t q_sh, int64_t
   a.o_sb = o_sb; a.o_sh = o_sh; a.o_sg = o_sg;
   a.B = B; a.KVH = KVH; a.G = G; a.cap = cap; a.splits = splits;
   a.scale_log2 = scale * kLog2e;
+  return QF_OK;
+}
 
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const int mode = splits == 1 ? kDirect : (ticket != nullptr ? kFused : kPartial);
-  const dim3 grid(splits, B * KVH);
-  const int nw = pick_waves(splits, B, KVH);
+static void launch_split_mode(const DecodeArgs& a, int mode, hipStream_t st) {
+  const dim3 grid(a.splits, a.B * a.KVH);
+  const int nw = pick_waves(a.splits, a.B, a.KVH);
   if (nw == 16) launch_nw<16>(a, mode, grid, st);
   else if (nw == 8) launch_nw<8>(a, mode, grid, st);
   else launch_nw<4>(a, mode, grid, st);
-  if (mode == kPartial) hipLaunchKernelGGL(decode_combine_kernel, dim3(B * KVH * G), dim3(256), 0, st, a);
+}
+
+static void launch_combine(const DecodeArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(decode_combine_kernel, dim3(a.B * a.KVH * a.G), dim3(256), 0, st, a);
+}
+
+extern "C" int qf_decode_attn(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sg,
+                              const void* k, int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                              const void* v, int64_t v_sb, int64_t v_sh, int64_t v_sn,
+                              const void* bias, int64_t bias_sb,
+                              const int64_t* kv_last, int64_t kv_last_sb,
+                              float* acc, float* m, float* l, int splits,
+                              int32_t* ticket,
+                              void* out, int64_t o_sb, int64_t o_sh, int64_t o_sg,
+                              int B, int KVH, int G, int D, int cap, float scale,
+                              void* stream) {
+  DecodeArgs a;
+  const int rc = make_args(a, q, q_sb, q_sh, q_sg, k, k_sb, k_sh, k_sn, v, v_sb, v_sh, v_sn,
+                           bias, bias_sb, kv_last, kv_last_sb, acc, m, l, splits, ticket, out,
+                           o_sb, o_sh, o_sg, B, KVH, G, D, cap, scale, true, true);
+  if (rc != QF_OK) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int mode = splits == 1 ? kDirect : (ticket != nullptr ? kFused : kPartial);
+  launch_split_mode(a, mode, st);
+  if (mode == kPartial) launch_combine(a, st);
+  return (int)hipGetLastError();
+}
+
+extern "C" int qf_decode_split(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sg,
+                               const void* k, int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                               const void* v, int64_t v_sb, int64_t v_sh, int64_t v_sn,
+                               const void* bias, int64_t bias_sb,
+                               const int64_t* kv_last, int64_t kv_last_sb,
+                               float* acc, float* m, float* l, int splits,
+                               int B, int KVH, int G, int D, int cap, float scale,
+                               void* stream) {
+  DecodeArgs a;
+  const int rc = make_args(a, q, q_sb, q_sh, q_sg, k, k_sb, k_sh, k_sn, v, v_sb, v_sh, v_sn,
+                           bias, bias_sb, kv_last, kv_last_sb, acc, m, l, splits, nullptr,
+                           nullptr, 0, 0, 0, B, KVH, G, D, cap, scale, true, false);
+  if (rc != QF_OK) return rc;
+  launch_split_mode(a, kPartial, static_cast<hipStream_t>(stream));
+  return (int)hipGetLastError();
+}
+
+extern "C" int qf_decode_combine(const float* acc, const float* m, const float* l, int splits,
+                                 void* out, int64_t o_sb, int64_t o_sh, int64_t o_sg,
+                                 int B, int KVH, int G, int D, void* stream) {
+  DecodeArgs a;
+  const int rc = make_args(a, nullptr, 0, 0, 0, nullptr, 0, 0, 0, nullptr, 0, 0, 0, nullptr, 0,
+                           nullptr, 0, const_cast<float*>(acc), const_cast<float*>(m),
+                           const_cast<float*>(l), splits, nullptr, out, o_sb, o_sh, o_sg, B, KVH,
+                           G, D, 1, 1.f, false, true);
+  if (rc != QF_OK) return rc;
+  launch_combine(a, static_cast<hipStream_t>(stream));
   return (int)hipGetLastError();
 }

@@ -104,21 +104,8 @@ def ticket_size(batch: int, kv_heads: int, splits: int) -> int:
     return batch * kv_heads * ((splits + 15) // 16 + 1)
 
 
-def flash_decode_attention(grouped: torch.Tensor, key_cache: torch.Tensor,
-                           value_cache: torch.Tensor, attn_bias: torch.Tensor | None,
-                           flash, kv_last: torch.Tensor | None = None,
-                           scale: float | None = None) -> torch.Tensor:
-    """Drop-in for ``StudentEngine._flash_decode_attention`` (SE:834-874).
-
-    grouped (B, KVH, G, D) fp16; key_cache/value_cache (B, KVH, cap, D) fp16;
-    attn_bias (B, cap) fp16 additive bias or None; ``flash`` is the
-    reference's ``(acc, m, l, out)`` static scratch -- the split count is
-    ``acc.shape[2]`` as in the reference -- optionally followed by an int32
-    ``ticket`` (see ``make_flash_scratch``) that selects the single-launch
-    merge.  ``kv_last`` (optional, device int64, shape (1,) or (B,)) is the
-    last slot that can be valid; slots after it are skipped (the engine passes
-    its ``write_index``).  Writes and returns ``out``.
-    """
+def _decode_args(grouped, key_cache, value_cache, attn_bias, flash, kv_last):
+    """Validate the decode operands; returns the parsed pieces."""
     acc, m, l, out = flash[:4]
     ticket = flash[4] if len(flash) > 4 else None
     _require_cuda_fp16("grouped", grouped, 4)
@@ -157,20 +144,83 @@ def flash_decode_attention(grouped: torch.Tensor, key_cache: torch.Tensor,
             kv_last_sb = kv_last.stride(0)
         else:
             raise ValueError("kv_last must hold 1 or B elements")
+    return acc, m, l, out, ticket, splits, cap, kv_last_sb
+
+
+def _qkv_bias_args(grouped, key_cache, value_cache, attn_bias, kv_last, kv_last_sb):
+    return (grouped.data_ptr(), grouped.stride(0), grouped.stride(1), grouped.stride(2),
+            key_cache.data_ptr(), key_cache.stride(0), key_cache.stride(1), key_cache.stride(2),
+            value_cache.data_ptr(), value_cache.stride(0), value_cache.stride(1), value_cache.stride(2),
+            _ptr(attn_bias), 0 if attn_bias is None else attn_bias.stride(0),
+            _ptr(kv_last), kv_last_sb)
+
+
+def flash_decode_attention(grouped: torch.Tensor, key_cache: torch.Tensor,
+                           value_cache: torch.Tensor, attn_bias: torch.Tensor | None,
+                           flash, kv_last: torch.Tensor | None = None,
+                           scale: float | None = None) -> torch.Tensor:
+    """Drop-in for ``StudentEngine._flash_decode_attention`` (SE:834-874).
+
+    grouped (B, KVH, G, D) fp16; key_cache/value_cache (B, KVH, cap, D) fp16;
+    attn_bias (B, cap) fp16 additive bias or None; ``flash`` is the
+    reference's ``(acc, m, l, out)`` static scratch -- the split count is
+    ``acc.shape[2]`` as in the reference -- optionally followed by an int32
+    ``ticket`` (see ``make_flash_scratch``) that selects the single-launch
+    merge.  ``kv_last`` (optional, device int64, shape (1,) or (B,)) is the
+    last slot that can be valid; slots after it are skipped (the engine passes
+    its ``write_index``).  Writes and returns ``out``.
+    """
+    acc, m, l, out, ticket, splits, cap, kv_last_sb = _decode_args(
+        grouped, key_cache, value_cache, attn_bias, flash, kv_last)
+    b, kvh, g, d = grouped.shape
     scale = d ** -0.5 if scale is None else scale
     lib = _lib.load()
     with torch.cuda.device(grouped.device):
         rc = lib.qf_decode_attn(
-            grouped.data_ptr(), grouped.stride(0), grouped.stride(1), grouped.stride(2),
-            key_cache.data_ptr(), key_cache.stride(0), key_cache.stride(1), key_cache.stride(2),
-            value_cache.data_ptr(), value_cache.stride(0), value_cache.stride(1), value_cache.stride(2),
-            _ptr(attn_bias), 0 if attn_bias is None else attn_bias.stride(0),
-            _ptr(kv_last), kv_last_sb,
+            *_qkv_bias_args(grouped, key_cache, value_cache, attn_bias, kv_last, kv_last_sb),
             acc.data_ptr(), m.data_ptr(), l.data_ptr(), splits,
             _ptr(ticket),
             out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
             b, kvh, g, d, cap, float(scale), _stream(grouped.device))
     _lib.check(rc, "qf_decode_attn")
+    return out
+
+
+def flash_decode_split(grouped, key_cache, value_cache, attn_bias, flash, kv_last=None,
+                       scale=None):
+    """The split launch alone (``_flash_decode_split_kernel``, SE:32-115 / SE:854-865):
+    fills the partials ``flash[0:3]`` = (acc, m, l)."""
+    acc, m, l, out, _, splits, cap, kv_last_sb = _decode_args(
+        grouped, key_cache, value_cache, attn_bias, flash, kv_last)
+    b, kvh, g, d = grouped.shape
+    scale = d ** -0.5 if scale is None else scale
+    lib = _lib.load()
+    with torch.cuda.device(grouped.device):
+        rc = lib.qf_decode_split(
+            *_qkv_bias_args(grouped, key_cache, value_cache, attn_bias, kv_last, kv_last_sb),
+            acc.data_ptr(), m.data_ptr(), l.data_ptr(), splits,
+            b, kvh, g, d, cap, float(scale), _stream(grouped.device))
+    _lib.check(rc, "qf_decode_split")
+    return acc, m, l
+
+
+def flash_decode_combine(flash):
+    """The combine launch alone (``_flash_decode_combine_kernel``, SE:117-162 /
+    SE:866-873): merges the partials of ``flash`` into ``flash[3]``."""
+    acc, m, l, out = flash[:4]
+    _require_cuda_fp16("out", out, 4)
+    b, kvh, splits, g, d = acc.shape
+    for name, t in (("acc", acc), ("m", m), ("l", l)):
+        if t.dtype != torch.float32 or not t.is_contiguous() or t.device != out.device:
+            raise ValueError(f"flash scratch {name} must be contiguous fp32 on {out.device}")
+    if m.shape != (b, kvh, splits, g) or l.shape != m.shape or out.shape != (b, kvh, g, d):
+        raise ValueError("flash scratch shapes do not match")
+    lib = _lib.load()
+    with torch.cuda.device(out.device):
+        rc = lib.qf_decode_combine(acc.data_ptr(), m.data_ptr(), l.data_ptr(), splits,
+                                   out.data_ptr(), out.stride(0), out.stride(1), out.stride(2),
+                                   b, kvh, g, d, _stream(out.device))
+    _lib.check(rc, "qf_decode_combine")
     return out
 
 

@@ -191,3 +191,15 @@ def test_graph_capture_replay(dev):
         ref = oracle.grouped_decode_attention(case.grouped.cpu(), case.key_cache[:, :, :last + 1].cpu(),
                                               case.value_cache[:, :, :last + 1].cpu())
         assert _err(got, ref) <= TOL, f"replay {step}"
+
+
+def test_split_then_combine_equals_attn(dev):
+    """The reference's two launches (SE:854-873) through the separate entry points."""
+    case = workloads.decode_ragged(4, seed=21)
+    c = case.to(dev)
+    flash = ops.make_flash_scratch(4, 2, 7, c.key_cache.shape[2], dev, splits=12, fused=False)
+    ops.flash_decode_split(c.grouped, c.key_cache, c.value_cache, c.bias, flash)
+    out = ops.flash_decode_combine(flash).float().cpu()
+    assert _err(out, _ref(case)) <= TOL
+    full = ops.flash_decode_attention(c.grouped, c.key_cache, c.value_cache, c.bias, flash)
+    assert torch.equal(full.float().cpu(), out)
