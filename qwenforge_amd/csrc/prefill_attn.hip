@@ -324,6 +324,295 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(Args a) {
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Streaming variant for K/V that are already rotated (and, in the fused op,
+// already in the cache): tiles go HBM -> LDS with asynchronous 16-byte
+// direct-to-LDS loads (global_load_lds) into a three-stage ring, so no
+// registers stage the data and two tiles are always in flight.  LDS rows are
+// 128 bytes, XOR-swizzled in 16-byte chunks (chunk c of row r lives at
+// c ^ swz(r)), which makes both the K operand reads (16 rows x 16 bytes per
+// lane group) and the transposing V reads conflict-free.  V^T operands come
+// from ds_read_b64_tr_b16: within each 16-lane group, lane i receives element
+// i % 4 of the 8-byte words addressed by lanes 4t + i/4 (t = 0..3), so lanes
+// that address 4 keys x 16 dims of V receive V^T[d][4 keys] directly.
+constexpr int kStages = 3;
+constexpr int kRowBytes = kD * 2;  // 128
+
+__device__ __forceinline__ int swz(int row) { return 2 * ((row >> 3) & 3) + ((row >> 1) & 1); }
+
+__device__ __forceinline__ void s_waitcnt_vm(int n) {
+  // gfx9 encoding: vmcnt[3:0] | expcnt=7 | lgkmcnt=15 | vmcnt[5:4] << 14.
+  if (n == 0) __builtin_amdgcn_s_waitcnt(0x0F70);
+  else __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4)
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+// ds_read_b64_tr_b16 of the 8-byte word at `p` (an LDS address).
+__device__ __forceinline__ f16x4 ds_read_tr16(const unsigned char* p) {
+  const i16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) i16x4*)(const_cast<unsigned char*>(p)));
+  return __builtin_bit_cast(f16x4, r);
+}
+
+// Per-lane state of the streaming prefill, shared by the three unrolled steps.
+struct LdsCtx {
+  const f16* kb;
+  const f16* vb;
+  const f16* kp[2];   // tile-0 source of this lane's two K rows (row lrow0 + 8i, its chunk)
+  const f16* vp[2];   // same for V
+  int64_t k_sn, v_sn;
+  int S, mt, qrow, n_ktiles, grp, lrow0, pch, w;
+  int koff[2][2][2];  // [ch][j][kk] LDS byte offsets of the K operand reads
+  int voff[2][4][2];  // [ch][d tile][h] LDS byte offsets of the V^T reads
+  f16x8 qf[2];
+  float m_use, ks2;
+  f32x4 l4;   // running sum of p per query column, kept by an MFMA against ones
+  f32x4 o[4];
+};
+
+// Async loads of tile kt (this wave's 16 rows of K and of V) into (Kd, Vd).
+__device__ __forceinline__ void lds_issue(const LdsCtx& c, int kt, unsigned char* Kd,
+                                          unsigned char* Vd) {
+  const int key0 = kt * kBN;
+  const bool tail = key0 + kBN > c.S;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const f16* ks;
+    const f16* vs;
+    if (!tail) {  // uniform: whole tile inside the sequence, pointer + scalar offset
+      ks = c.kp[i] + key0 * c.k_sn;
+      vs = c.vp[i] + key0 * c.v_sn;
+    } else {      // last tile: rows past the sequence repeat row S-1 (masked later)
+      const int r = c.lrow0 + 8 * i;
+      const int ch = c.pch ^ swz(r);
+      int key = key0 + r;
+      key = key < c.S ? key : c.S - 1;
+      ks = c.kb + (int64_t)key * c.k_sn + 8 * ch;
+      vs = c.vb + (int64_t)key * c.v_sn + 8 * ch;
+    }
+    __builtin_amdgcn_global_load_lds(ks, (lds_void*)(Kd + (16 * c.w + 8 * i) * kRowBytes), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(vs, (lds_void*)(Vd + (16 * c.w + 8 * i) * kRowBytes), 16, 0, 0);
+  }
+}
+
+// One tile: wait for its loads, refill the stage of tile kt-1 with tile kt+2,
+// then scores, online softmax and PV from (Ks, Vs).
+__device__ __forceinline__ void lds_step(LdsCtx& c, int kt, const unsigned char* Ks,
+                                         const unsigned char* Vs, unsigned char* Kn,
+                                         unsigned char* Vn) {
+  const int key0 = kt * kBN;
+  // This wave's loads of tile kt have landed (the loads of tile kt+1 may stay
+  // in flight); after the barrier every wave's have, and every wave is done
+  // reading tile kt-1, whose stage is refilled with tile kt+2.  The barrier is
+  // bare (a workgroup fence would wait for all outstanding LDS loads); the
+  // signal fences keep the compiler from moving LDS accesses across it.
+  s_waitcnt_vm(kt + 1 < c.n_ktiles ? 4 : 0);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+
+  f16x8 ka[2][2][2];
+#pragma unroll
+  for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+        ka[ch][j][kk] = *reinterpret_cast<const f16x8*>(Ks + c.koff[ch][j][kk]);
+  // Refill after the K operands are in registers (the V^T reads come later).
+  if (kt + 2 < c.n_ktiles) lds_issue(c, kt + 2, Kn, Vn);
+  f32x4 sc[4];
+#pragma unroll
+  for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      acc = mfma16x16x32(ka[ch][j][0], c.qf[0], acc);
+      sc[2 * ch + j] = mfma16x16x32(ka[ch][j][1], c.qf[1], acc);
+    }
+  if (key0 + kBN > c.mt * kBM || key0 + kBN > c.S) {  // diagonal or tail tile: mask
+#pragma unroll
+    for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = key0 + 32 * (blk >> 1) + 8 * c.grp + 4 * (blk & 1) + i;
+        if (!(key <= c.qrow && key < c.S)) sc[blk][i] = kNegInf;
+      }
+  }
+  float mx = fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3]));
+#pragma unroll
+  for (int blk = 1; blk < 4; ++blk)
+    mx = fmaxf(mx, fmaxf(fmaxf(sc[blk][0], sc[blk][1]), fmaxf(sc[blk][2], sc[blk][3])));
+  mx *= c.ks2;
+  if (__any(mx > c.m_use + kRescaleSlack)) {
+    const float m_new = fmaxf(c.m_use, col_max(mx));
+    const float resc = (m_new == kNegInf) ? 1.f : fast_exp2(c.m_use - m_new);
+    c.l4 *= resc;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) c.o[t] *= resc;
+    c.m_use = m_new;
+  }
+  const float neg_m = (c.m_use == kNegInf) ? 0.f : -c.m_use;
+  f16x8 pb[2];
+#pragma unroll
+  for (int blk = 0; blk < 4; ++blk)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float p = fast_exp2(__builtin_fmaf(sc[blk][i], c.ks2, neg_m));  // 0 for masked keys
+      pb[blk >> 1][4 * (blk & 1) + i] = (f16)p;
+    }
+  // Row sums of P^T on the matrix core: ones x P^T puts sum_k p[k][q] in every
+  // row of column q, already reduced over the four lanes of the column, and
+  // over the same fp16 p the PV product uses.
+  const f16x8 ones = {(f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f};
+  c.l4 = mfma16x16x32(ones, pb[0], c.l4);
+  c.l4 = mfma16x16x32(ones, pb[1], c.l4);
+#pragma unroll
+  for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const f16x4 lo = ds_read_tr16(Vs + c.voff[ch][t][0]);
+      const f16x4 hi = ds_read_tr16(Vs + c.voff[ch][t][1]);
+      const f16x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      c.o[t] = mfma16x16x32(va, pb[ch], c.o[t]);
+    }
+}
+
+template <bool kRopeQ>
+__global__ __launch_bounds__(kWaves * 64) void prefill_lds_kernel(Args a) {
+  // Three stages, each its own K and V array so that loads into one stage are
+  // visibly disjoint from reads of another (no conservative waits).
+  __shared__ __attribute__((aligned(16))) unsigned char k0[kBN * kRowBytes], v0[kBN * kRowBytes];
+  __shared__ __attribute__((aligned(16))) unsigned char k1[kBN * kRowBytes], v1[kBN * kRowBytes];
+  __shared__ __attribute__((aligned(16))) unsigned char k2[kBN * kRowBytes], v2[kBN * kRowBytes];
+
+  const int n_mtiles = gridDim.x;
+  const int mt = n_mtiles - 1 - blockIdx.x;  // heaviest tiles first
+  const int bq = blockIdx.y;
+  const int b = bq / a.QH, hq = bq % a.QH;
+  const int hk = hq / a.G;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
+  const int col = lane & 15, grp = lane >> 4;
+  const int S = a.S;
+
+  LdsCtx c;
+  c.kb = a.k + b * a.k_sb + hk * a.k_sh;
+  c.vb = a.v + b * a.v_sb + hk * a.v_sh;
+  c.k_sn = a.k_sn;
+  c.v_sn = a.v_sn;
+  c.S = S;
+  c.mt = mt;
+  c.grp = grp;
+  c.w = w;
+  const int key_end = (mt + 1) * kBM < S ? (mt + 1) * kBM : S;
+  c.n_ktiles = (key_end + kBN - 1) / kBN;
+  c.qrow = mt * kBM + w * 16 + col;
+  // Loader mapping: lane -> row 8i + lane/8 of the wave's 16, physical chunk lane % 8.
+  c.lrow0 = 16 * w + (lane >> 3);
+  c.pch = lane & 7;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = c.lrow0 + 8 * i;
+    const int ch = c.pch ^ swz(r);
+    c.kp[i] = c.kb + (int64_t)r * c.k_sn + 8 * ch;
+    c.vp[i] = c.vb + (int64_t)r * c.v_sn + 8 * ch;
+  }
+
+  // ---- Q^T operand (16 rows per wave), rotated in registers; loads go first.
+  f16x8 qcs[4];
+  {
+    const int qr = c.qrow < S ? c.qrow : S - 1;
+    const f16* qp = a.q + b * a.q_sb + hq * a.q_sh + (int64_t)qr * a.q_sn + 8 * grp;
+    c.qf[0] = load16(qp);
+    c.qf[1] = load16(qp + 32);
+    if (kRopeQ) {
+      const int64_t co = b * a.cs_sb + (int64_t)qr * a.cs_sn + 8 * grp;
+      qcs[0] = load16(a.cos + co);
+      qcs[1] = load16(a.sin + co);
+      qcs[2] = load16(a.cos + co + 32);
+      qcs[3] = load16(a.sin + co + 32);
+    }
+  }
+  lds_issue(c, 0, k0, v0);
+  if (c.n_ktiles > 1) lds_issue(c, 1, k1, v1);
+  if (kRopeQ) rope_pair(c.qf[0], c.qf[1], qcs[0], qcs[1], qcs[2], qcs[3]);
+
+#pragma unroll
+  for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int r = 32 * ch + 8 * (col >> 2) + 4 * j + (col & 3);
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) c.koff[ch][j][kk] = r * kRowBytes + 16 * ((grp + 4 * kk) ^ swz(r));
+    }
+#pragma unroll
+  for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int r = 32 * ch + 8 * grp + 4 * h + (col >> 2);
+        const int d = 16 * t + 4 * (col & 3);
+        c.voff[ch][t][h] = r * kRowBytes + 16 * ((d >> 3) ^ swz(r)) + 2 * (d & 7);
+      }
+  c.m_use = kNegInf;
+  c.l4 = f32x4{0.f, 0.f, 0.f, 0.f};
+  c.ks2 = a.scale_log2;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) c.o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int kt = 0; kt < c.n_ktiles; kt += kStages) {
+    lds_step(c, kt, k0, v0, k2, v2);
+    if (kt + 1 < c.n_ktiles) lds_step(c, kt + 1, k1, v1, k0, v0);
+    if (kt + 2 < c.n_ktiles) lds_step(c, kt + 2, k2, v2, k1, v1);
+  }
+
+  const float l_run = c.l4[0];
+  if (c.qrow < S) {
+    const float inv = 1.f / l_run;
+    f16* op = a.out + b * a.o_sb + hq * a.o_sh + (int64_t)c.qrow * a.o_sn;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      f16x4 r;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) r[i] = (f16)(c.o[t][i] * inv);
+      *reinterpret_cast<f16x4*>(op + 16 * t + 4 * grp) = r;
+    }
+  }
+}
+
+// Pre-pass of the fused op: rotated K and raw V of every token into the cache
+// at slots start_pos + i (bit-exact eager rounding), so the attention kernel
+// streams finished rows.  Block = 16 tokens x (4 K chunk pairs + 8 V chunks).
+__global__ __launch_bounds__(256) void rope_kv_prefill_kernel(Args a) {
+  const int tok = blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int sub = threadIdx.x & 15;
+  const int bh = blockIdx.y;
+  const int b = bh / a.KVH, h = bh % a.KVH;
+  if (tok >= a.S || sub >= 12) return;
+  const int64_t slot = a.start_pos + tok;
+  if (sub < 4) {
+    const f16* src = a.k + b * a.k_sb + h * a.k_sh + (int64_t)tok * a.k_sn + 8 * sub;
+    f16x8 lo = load16(src), hi = load16(src + 32);
+    if (a.cos != nullptr) {
+      const int64_t co = b * a.cs_sb + (int64_t)tok * a.cs_sn + 8 * sub;
+      rope_pair(lo, hi, load16(a.cos + co), load16(a.sin + co), load16(a.cos + co + 32),
+                load16(a.sin + co + 32));
+    }
+    f16* dst = a.kc + b * a.kc_sb + h * a.kc_sh + slot * a.kc_sn + 8 * sub;
+    store16(dst, lo);
+    store16(dst + 32, hi);
+  } else {
+    const int c = sub - 4;
+    store16(a.vc + b * a.vc_sb + h * a.vc_sh + slot * a.vc_sn + 8 * c,
+            load16(a.v + b * a.v_sb + h * a.v_sh + (int64_t)tok * a.v_sn + 8 * c));
+  }
+}
+
 }  // namespace prefill
 }  // namespace qf
 
@@ -381,9 +670,23 @@ extern "C" int qf_prefill_attn(const void* q, int64_t q_sb, int64_t q_sh, int64_
 
   hipStream_t st = static_cast<hipStream_t>(stream);
   dim3 grid((S + kBM - 1) / kBM, B * QH), block(kWaves * 64);
-  if (rope && append) hipLaunchKernelGGL((prefill_kernel<true, true>), grid, block, 0, st, a);
-  else if (rope) hipLaunchKernelGGL((prefill_kernel<true, false>), grid, block, 0, st, a);
-  else if (append) hipLaunchKernelGGL((prefill_kernel<false, true>), grid, block, 0, st, a);
-  else hipLaunchKernelGGL((prefill_kernel<false, false>), grid, block, 0, st, a);
+  if (rope && !append) {
+    // No cache to hold the rotated keys: rotate K in registers tile by tile.
+    hipLaunchKernelGGL((prefill_kernel<true, false>), grid, block, 0, st, a);
+    return (int)hipGetLastError();
+  }
+  if (append) {
+    // Pre-pass: rotated K (or K as is) and V into the cache; then stream the
+    // finished rows back from the cache.
+    Args pre = a;
+    hipLaunchKernelGGL(rope_kv_prefill_kernel, dim3((S + 15) / 16, B * KVH), dim3(256), 0, st,
+                       pre);
+    a.k = a.kc + start_pos * a.kc_sn;
+    a.k_sb = kc_sb; a.k_sh = kc_sh; a.k_sn = kc_sn;
+    a.v = a.vc + start_pos * a.vc_sn;
+    a.v_sb = vc_sb; a.v_sh = vc_sh; a.v_sn = vc_sn;
+  }
+  if (rope) hipLaunchKernelGGL((prefill_lds_kernel<true>), grid, block, 0, st, a);
+  else hipLaunchKernelGGL((prefill_lds_kernel<false>), grid, block, 0, st, a);
   return (int)hipGetLastError();
 }
