@@ -1,4 +1,4 @@
-"""ctypes binding of the C ABI in ``include/qf_attn.h``.
+"""ctypes binding of the C ABI in ``include/qf_attn.h`` and ``include/qf_step.h``.
 
 The shared object is built in-tree by ``qwenforge_amd.build``.  There is no
 fallback: if it is missing or does not load, every op raises.
@@ -66,6 +66,44 @@ SIGNATURES = {
         _vp,                            # write_index
         _vp, _i64, _i64,                # q_out
         _i32, _i32, _i32, _i32, _i32,   # B, QH, KVH, D, cap
+        _vp,                            # stream
+    ],
+    # include/qf_step.h
+    "qf_rms_qkv_rope_append": [
+        _vp, _i64, _vp,                 # x, x_sb, token
+        _vp, _i64,                      # hidden_out, ho_sb
+        _vp, _f32,                      # norm_w, eps
+        _vp, _vp,                       # w_qkv, bias
+        _vp, _vp, _i64,                 # cos, sin, cs_sb
+        _vp, _i64, _i64, _i64,          # k_cache
+        _vp, _i64, _i64, _i64,          # v_cache
+        _vp,                            # write_index
+        _vp, _i64, _i64,                # q_out, qo_sb, qo_sh
+        _i32, _i32, _i32, _i32, _i32, _i32,  # B, hidden, QH, KVH, D, cap
+        _vp,                            # stream
+    ],
+    "qf_gemv_residual": [
+        _vp, _i64, _vp,                 # inp, in_sb, w
+        _vp, _i64,                      # hidden, h_sb
+        _i32, _i32, _i32,               # B, K, N
+        _vp,                            # stream
+    ],
+    "qf_rms_gate_up_swiglu": [
+        _vp, _i64, _vp, _f32,           # x, x_sb, norm_w, eps
+        _vp, _vp, _i64,                 # w_gate_up, h_out, ho_sb
+        _i32, _i32, _i32,               # B, hidden, I
+        _vp,                            # stream
+    ],
+    "qf_rms_lm_head": [
+        _vp, _i64, _vp, _f32,           # x, x_sb, norm_w, eps
+        _vp, _vp, _i64, _vp,            # w_lm, logits, lg_sb, keys
+        _i32, _i32, _i32, _i32,         # n_blocks, B, hidden, V
+        _vp,                            # stream
+    ],
+    "qf_argmax_step": [
+        _vp, _i32, _i32, _vp,           # keys, n_blocks, B, token
+        _vp, _i64, _i32,                # rows, rows_sb, n_rows
+        _vp, _vp, _vp,                  # step, write_index, pos
         _vp,                            # stream
     ],
     "qf_error_string": [_i32],

@@ -15,8 +15,14 @@ Mirrors the reference's cached generation path without the tokenizer:
   replays (bias slot, write slot, positions, token store; SE:1126-1132) runs
   inside the graph as device ops, so a step is a single graph replay.
 
-GEMMs, RMSNorm and SwiGLU stay torch ops (hipBLASLt / ATen kernels), as in the
-reference.  Everything is fp16 storage with the reference's op order.
+For batches of 1..4 rows the decode step body is the fused weight-streaming
+path (``step_ops``, include/qf_step.h): per layer one launch for rms_norm +
+QKV + RoPE + append, the attention launch(es), one for o_proj + residual, one
+for rms_norm + gate/up + SwiGLU and one for down_proj + residual; then one
+for rms_norm + lm_head + per-block argmax and one for the argmax and the slot
+bookkeeping.  Larger batches keep the torch projections (hipBLASLt / ATen
+kernels) around the same HIP attention kernels.  Prefill always uses the torch
+projections.  Everything is fp16 storage with the reference's rounding points.
 """
 
 from __future__ import annotations
@@ -24,7 +30,7 @@ from __future__ import annotations
 import torch
 import torch.nn.functional as F
 
-from . import ops
+from . import ops, step_ops
 from .model import Qwen2Config
 from .rope import cos_sin, inv_freq
 
@@ -32,13 +38,19 @@ from .rope import cos_sin, inv_freq
 class DecodeEngine:
     """Batched greedy decoding of a Qwen2-shaped model on one MI355X."""
 
-    def __init__(self, cfg: Qwen2Config, weights: dict, device="cuda"):
+    def __init__(self, cfg: Qwen2Config, weights: dict, device="cuda", fused_step: bool = True):
         self.cfg = cfg
         self.device = torch.device(device)
         self.w = weights
         self.inv_freq = inv_freq(cfg.head_dim, cfg.rope_theta, self.device)
         self.scale = cfg.head_dim ** -0.5
+        self.fused_step = fused_step
         self._ctx = None
+
+    def uses_fused_step(self, batch: int) -> bool:
+        """The fused decode-step kernels cover 1..4 rows and hidden <= 1024."""
+        return (self.fused_step and 1 <= batch <= step_ops.MAX_BATCH and self.cfg.hidden <= 1024
+                and self.cfg.head_dim == step_ops.HEAD_DIM)
 
     # ------------------------------------------------------------------ helpers
     def _rms(self, x, weight):
@@ -89,6 +101,44 @@ class DecodeEngine:
     # ------------------------------------------------------------------ decode
     def _step(self, ctx):
         """One static-shape decode step (the captured graph body)."""
+        if ctx.get("fused"):
+            self._step_fused(ctx)
+        else:
+            self._step_torch(ctx)
+
+    def _step_fused(self, ctx):
+        """The step body on the fused weight-streaming kernels (B <= 4)."""
+        cfg = self.cfg
+        b = ctx["token"].shape[0]
+        eps = cfg.rms_eps
+        if ctx["bias"] is not None:
+            ctx["bias"].index_fill_(1, ctx["write"], 0.0)
+        cos, sin = cos_sin(ctx["pos"], self.inv_freq)          # (B, D), once per step (SE:910-915)
+        hidden, q_rot, h = ctx["hidden"], ctx["q_rot"], ctx["h"]
+        for i, (layer, (kc, vc)) in enumerate(zip(self.w["layers"], ctx["caches"])):
+            if i == 0:
+                # Embedding gather (SE:896) folded into the first projection.
+                step_ops.rms_qkv_rope_append(self.w["embed"], layer["input_norm"], eps,
+                                             layer["qkv_weight"], layer["qkv_bias"], cos, sin,
+                                             kc, vc, ctx["write"], q_rot, token=ctx["token"],
+                                             hidden_out=hidden)
+            else:
+                step_ops.rms_qkv_rope_append(hidden, layer["input_norm"], eps, layer["qkv_weight"],
+                                             layer["qkv_bias"], cos, sin, kc, vc, ctx["write"],
+                                             q_rot)
+            grouped = q_rot.view(b, cfg.kv_heads, cfg.groups, cfg.head_dim)
+            att = ops.flash_decode_attention(grouped, kc, vc, ctx["bias"], ctx["flash"],
+                                             kv_last=ctx["write"], scale=self.scale)
+            step_ops.gemv_residual(att.view(b, cfg.hidden), layer["o_weight"], hidden)
+            step_ops.rms_gate_up_swiglu(hidden, layer["post_norm"], eps, layer["gate_up_weight"], h)
+            step_ops.gemv_residual(h, layer["down_weight"], hidden)
+        step_ops.rms_lm_head(hidden, self.w["final_norm"], eps, self.w["lm_head"], ctx["logits"],
+                             ctx["keys"])
+        step_ops.argmax_step(ctx["keys"], ctx["token"], ctx["rows"], ctx["step"], ctx["write"],
+                             ctx["pos"])
+
+    def _step_torch(self, ctx):
+        """The step body on torch projections around the HIP attention kernels."""
         cfg = self.cfg
         b = ctx["token"].shape[0]
         if ctx["bias"] is not None:
@@ -128,7 +178,7 @@ class DecodeEngine:
             bias = torch.full((batch, cap), torch.finfo(torch.float16).min, device=dev,
                               dtype=torch.float16)
             bias.masked_fill_(bias_mask, 0.0)
-        return {
+        ctx = {
             "caches": caches,
             "bias": bias,
             "flash": ops.make_flash_scratch(batch, cfg.kv_heads, cfg.groups, cap, dev),
@@ -138,7 +188,15 @@ class DecodeEngine:
             "step": torch.zeros(1, device=dev, dtype=torch.long),
             "rows": torch.zeros(batch, max_new_tokens, device=dev, dtype=torch.long),
             "logits": torch.zeros(batch, cfg.vocab, device=dev, dtype=torch.float16),
+            "fused": self.uses_fused_step(batch),
         }
+        if ctx["fused"]:
+            f16 = torch.float16
+            ctx["hidden"] = torch.zeros(batch, cfg.hidden, device=dev, dtype=f16)
+            ctx["q_rot"] = torch.zeros(batch, cfg.heads, cfg.head_dim, device=dev, dtype=f16)
+            ctx["h"] = torch.zeros(batch, cfg.intermediate, device=dev, dtype=f16)
+            ctx["keys"] = torch.zeros(batch, step_ops.LM_BLOCKS, device=dev, dtype=torch.long)
+        return ctx
 
     def capture(self, ctx):
         """Capture ``_step`` into a hipGraph (2 warm-ups on a side stream, SE:1056-1074).

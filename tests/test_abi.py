@@ -12,18 +12,23 @@ import pytest
 
 from qwenforge_amd import _lib
 
-HEADER = Path(__file__).resolve().parents[1] / "include" / "qf_attn.h"
+INCLUDE = Path(__file__).resolve().parents[1] / "include"
+HEADERS = sorted(INCLUDE.glob("*.h"))
 
 
 def _declared():
-    text = HEADER.read_text()
-    return sorted(set(re.findall(r"^\s*(?:const\s+char\*|int)\s+(qf_\w+)\s*\(", text, re.M)))
+    names = set()
+    for header in HEADERS:
+        text = header.read_text()
+        names.update(re.findall(r"^\s*(?:const\s+char\*|int)\s+(qf_\w+)\s*\(", text, re.M))
+    return sorted(names)
 
 
 def test_header_declares_the_three_kernels():
     names = _declared()
     for n in ("qf_decode_attn", "qf_prefill_attn", "qf_rope_append", "qf_error_string",
-              "qf_abi_version"):
+              "qf_abi_version", "qf_rms_qkv_rope_append", "qf_gemv_residual",
+              "qf_rms_gate_up_swiglu", "qf_rms_lm_head", "qf_argmax_step"):
         assert n in names
 
 
@@ -101,3 +106,26 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     with pytest.raises(RuntimeError, match="missing"):
         _lib.load()
     assert ctypes  # keeps the import used
+
+
+def test_step_kernels_reject_bad_arguments():
+    lib = _lib.load()
+    # B outside 1..4 and hidden > 1024 are unsupported; null pointers invalid.
+    assert lib.qf_gemv_residual(16, 896, 16, 16, 896, 5, 896, 896, None) == -2
+    assert lib.qf_gemv_residual(16, 896, 16, 16, 896, 1, 8200, 896, None) == -2
+    assert lib.qf_gemv_residual(None, 896, 16, 16, 896, 1, 896, 896, None) == -1
+    assert lib.qf_gemv_residual(18, 896, 16, 16, 896, 1, 896, 896, None) == -1  # misaligned
+    assert lib.qf_rms_gate_up_swiglu(16, 896, 16, 1e-6, 16, 16, 4864, 1, 2048, 4864, None) == -2
+    assert lib.qf_rms_gate_up_swiglu(16, 896, None, 1e-6, 16, 16, 4864, 1, 896, 4864, None) == -1
+    assert lib.qf_rms_lm_head(16, 896, 16, 1e-6, 16, 16, 100, 16, 0, 1, 896, 100, None) == -1
+    assert lib.qf_rms_lm_head(16, 896, 16, 1e-6, 16, 16, 100, 16, 8, 0, 896, 100, None) == -2
+    assert lib.qf_argmax_step(16, 8, 1, 16, 16, 4, 4, None, None, None, None) == -1  # rows w/o step
+    assert lib.qf_argmax_step(16, 8, 9, 16, None, 0, 0, None, None, None, None) == -2
+    rc = lib.qf_rms_qkv_rope_append(16, 896, None, None, 0, 16, 1e-6, 16, None, 16, 16, 64,
+                                    16, 0, 0, 0, 16, 0, 0, 0, 16, 16, 0, 0,
+                                    1, 896, 14, 2, 128, 64, None)
+    assert rc == -2  # head_dim 128
+    rc = lib.qf_rms_qkv_rope_append(16, 896, None, None, 0, 16, 1e-6, 16, None, 16, 16, 64,
+                                    None, 0, 0, 0, 16, 0, 0, 0, 16, 16, 0, 0,
+                                    1, 896, 14, 2, 64, 64, None)
+    assert rc == -1  # no key cache

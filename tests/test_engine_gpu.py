@@ -101,3 +101,42 @@ def test_generate_full_shape_runs(dev):
     assert rows.shape == (4, 16)
     assert int(rows.min()) >= 0 and int(rows.max()) < cfg.vocab
     assert timing["decode_ms"] > 0
+
+
+def test_fused_step_matches_torch_step(dev):
+    """The fused weight-streaming step and the torch-projection step agree
+    (teacher-forced: both are fed the same tokens every step)."""
+    cfg = Qwen2Config(layers=4)
+    w = init_weights(cfg, dev, seed=3)
+    b, s, steps = 2, 100, 3
+    gen = torch.Generator().manual_seed(5)
+    ids = torch.randint(0, cfg.vocab, (b, s), generator=gen).to(dev)
+    teacher = torch.randint(0, cfg.vocab, (steps, b), generator=gen).to(dev)
+    out = {}
+    for fused in (True, False):
+        eng = DecodeEngine(cfg, w, dev, fused_step=fused)
+        caches = eng.new_caches(b, 192)
+        eng.prefill(ids, caches)
+        ctx = eng.make_context(caches, b, steps + 1)
+        assert ctx["fused"] == fused
+        ctx["pos"].fill_(s)
+        ctx["write"].fill_(s)
+        ctx["step"].fill_(1)
+        logits = []
+        for t in range(steps):
+            ctx["token"].copy_(teacher[t])
+            eng._step(ctx)
+            logits.append(ctx["logits"].float().cpu())
+        torch.cuda.synchronize()
+        out[fused] = (torch.stack(logits), int(ctx["write"].item()), ctx["pos"].cpu(),
+                      int(ctx["step"].item()),
+                      [(k[:, :, s:s + steps].float().cpu(), v[:, :, s:s + steps].float().cpu())
+                       for k, v in caches])
+    (lf, wf, pf, sf, cf), (lt, wt, pt, st, ct) = out[True], out[False]
+    err = (lf - lt).abs().max().item()
+    print(f"[fused vs torch step] max|dlogit| {err:.3e}", flush=True)
+    assert err <= LOGIT_TOL
+    assert wf == wt == s + steps and sf == st == 1 + steps and torch.equal(pf, pt)
+    for (kf, vf), (kt, vt) in zip(cf, ct):
+        assert (kf - kt).abs().max().item() <= 2e-2
+        assert (vf - vt).abs().max().item() <= 2e-2
