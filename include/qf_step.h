@@ -61,6 +61,19 @@ int qf_rms_qkv_rope_append(const void* x, int64_t x_sb, const int64_t* token,
 int qf_gemv_residual(const void* inp, int64_t in_sb, const void* w,
                      void* hidden, int64_t h_sb, int B, int K, int N, void* stream);
 
+/* Split-K attention merge + o_proj + residual.  Replaces the second decode
+ * launch _flash_decode_combine_kernel (student_engine.py:117-162, launched at
+ * :860-872) together with `hidden = residual + F.linear(attended, o_weight)`
+ * (:973-974): every workgroup merges the partials (acc, m, l) of
+ * qf_decode_split for all B x KVH x G query heads, rounds the merged rows to
+ * fp16 as the combine does (fp16(A * (1/L))) and applies the projection.
+ * acc: (B, KVH, splits, G, 64) fp32, m/l: (B, KVH, splits, G) fp32 (m in
+ * natural-log units), all contiguous; w_o: (N, KVH*G*64); hidden: (B, N) row
+ * stride h_sb, updated in place.  Supports KVH*G*64 <= 1024, B in 1..4. */
+int qf_attn_merge_o_proj(const float* acc, const float* m, const float* l, int splits,
+                         int KVH, int G, const void* w_o, void* hidden, int64_t h_sb,
+                         int B, int N, void* stream);
+
 /* RMSNorm + gate/up projection + SwiGLU.  Replaces `normalized =
  * rms_norm(hidden, post_norm)` (:976-977) and the first two lines of _mlp
  * (:664-665) plus the product `gate * up` (:666): h = fp16(fp16(silu(g)) * u)

@@ -88,6 +88,13 @@ SIGNATURES = {
         _i32, _i32, _i32,               # B, K, N
         _vp,                            # stream
     ],
+    "qf_attn_merge_o_proj": [
+        _vp, _vp, _vp, _i32,            # acc, m, l, splits
+        _i32, _i32,                     # KVH, G
+        _vp, _vp, _i64,                 # w_o, hidden, h_sb
+        _i32, _i32,                     # B, N
+        _vp,                            # stream
+    ],
     "qf_rms_gate_up_swiglu": [
         _vp, _i64, _vp, _f32,           # x, x_sb, norm_w, eps
         _vp, _vp, _i64,                 # w_gate_up, h_out, ho_sb

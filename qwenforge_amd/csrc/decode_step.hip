@@ -48,10 +48,24 @@ __device__ __forceinline__ float dot8(f16x8 w, f16x8 x, float acc) {
   return acc;
 }
 
+// Sum over the 64 lanes with DPP moves (no LDS traffic): butterflies inside
+// each 16-lane row, then row broadcasts leave the total in lane 63, which is
+// read back as a wave-uniform value.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ float dpp_add(float v) {
+  const int moved = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, kRowMask, 0xF,
+                                                false);
+  return v + __builtin_bit_cast(float, moved);
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-  return v;
+  v = dpp_add<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+  v = dpp_add<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]: quad sums
+  v = dpp_add<0x141, 0xF>(v);  // row_half_mirror: 8-lane sums
+  v = dpp_add<0x140, 0xF>(v);  // row_mirror: 16-lane row sums
+  v = dpp_add<0x142, 0xA>(v);  // row_bcast:15 into rows 1, 3
+  v = dpp_add<0x143, 0xC>(v);  // row_bcast:31 into rows 2, 3: lane 63 holds the total
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 __device__ __forceinline__ f16x8 zero8() {
@@ -62,14 +76,16 @@ __device__ __forceinline__ f16x8 zero8() {
 }
 
 // The NS 16-byte chunks of one weight row that lane `lane` multiplies:
-// chunk 64*s + lane, s < NS (chunks past the row are zero).
+// chunk 64*s + lane, s < NS.  Lanes past the row's C chunks load its last
+// chunk (never used), so no load sits behind a branch and every load of a
+// wave is in flight at once.
 template <int NS>
 __device__ __forceinline__ void load_row(const f16* __restrict__ w, int C, f16x8 (&r)[NS],
                                          int lane) {
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
-    const int c = 64 * s + lane;
-    r[s] = c < C ? load16(w + 8 * c) : zero8();
+    const int c = min(64 * s + lane, C - 1);
+    r[s] = load16(w + 8 * c);
   }
 }
 
@@ -79,42 +95,54 @@ __device__ __forceinline__ void dot_row(const f16x8 (&r)[NS], const f16* xs, int
                                         float (&acc)[NB], int lane) {
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
-    const int c = 64 * s + lane;
-    if (c < C) {
+    const int c0 = 64 * s + lane;
+    const bool in = c0 < C;
+    const int c = in ? c0 : C - 1;
+    const f16x8 wv = in ? r[s] : zero8();
 #pragma unroll
-      for (int b = 0; b < NB; ++b)
-        acc[b] = dot8(r[s], *reinterpret_cast<const f16x8*>(xs + b * K + 8 * c), acc[b]);
-    }
+    for (int b = 0; b < NB; ++b)
+      acc[b] = dot8(wv, *reinterpret_cast<const f16x8*>(xs + b * K + 8 * c), acc[b]);
   }
 }
 
-// Stages NB activation rows into LDS xs[b * K ..], RMS-normalised as torch's
-// fused RMSNorm kernel does for fp16 (fp32 math, one rounding):
+// RMS-normalised staging of NB activation rows into LDS xs[b * K ..], as
+// torch's fused RMSNorm kernel computes it for fp16 (fp32 math, one rounding):
 //   y = fp16((x * rsqrt(mean(x^2) + eps)) * w)     (student_engine.py:530-535 form)
-// K <= kMaxNormK, so each thread owns at most one chunk per row.  When
-// `raw_out` is non-null the unnormalised rows are also copied there.
+// Split in two so the caller can issue its weight loads in between: the
+// activation loads go first and are waited for alone.  K <= kMaxNormK, so
+// thread t < C owns chunk t of every row.
 template <int NB>
-__device__ __forceinline__ void stage_rms(const f16* const (&rows)[NB], int K,
-                                          const f16* __restrict__ nw, float eps, f16* xs,
-                                          float* red, f16* raw_out, int64_t raw_sb) {
+struct RmsStage {
+  f16x8 x[NB];
+  f16x8 g;
+};
+
+template <int NB>
+__device__ __forceinline__ void rms_load(RmsStage<NB>& st, const f16* const (&rows)[NB], int K,
+                                         const f16* __restrict__ nw) {
+  const int c = min((int)threadIdx.x, K / 8 - 1);
+  st.g = load16(nw + 8 * c);
+#pragma unroll
+  for (int b = 0; b < NB; ++b) st.x[b] = load16(rows[b] + 8 * c);
+}
+
+template <int NB>
+__device__ __forceinline__ void rms_finish(const RmsStage<NB>& st, int K, float eps, f16* xs,
+                                           float* red, f16* raw_out, int64_t raw_sb) {
   const int C = K / 8;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  f16x8 xv[NB];
-  float ss[NB];
   const bool own = tid < C;
-  const f16x8 g = own ? load16(nw + 8 * tid) : zero8();
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
-    xv[b] = own ? load16(rows[b] + 8 * tid) : zero8();
     float s = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) s += (float)xv[b][e] * (float)xv[b][e];
-    ss[b] = wave_sum(s);
-    if (lane == 0) red[w * NB + b] = ss[b];
+    for (int e = 0; e < 8; ++e) s += (float)st.x[b][e] * (float)st.x[b][e];
+    s = wave_sum(own ? s : 0.f);
+    if (lane == 0) red[w * NB + b] = s;
   }
   if (raw_out != nullptr && own) {
 #pragma unroll
-    for (int b = 0; b < NB; ++b) store16(raw_out + b * raw_sb + 8 * tid, xv[b]);
+    for (int b = 0; b < NB; ++b) store16(raw_out + b * raw_sb + 8 * tid, st.x[b]);
   }
   __syncthreads();
   if (own) {
@@ -126,21 +154,34 @@ __device__ __forceinline__ void stage_rms(const f16* const (&rows)[NB], int K,
       const float rstd = rsqrtf(tot / (float)K + eps);
       f16x8 y;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) y[e] = (f16)(((float)xv[b][e] * rstd) * (float)g[e]);
+      for (int e = 0; e < 8; ++e) y[e] = (f16)(((float)st.x[b][e] * rstd) * (float)st.g[e]);
       store16(xs + b * K + 8 * tid, y);
     }
   }
   __syncthreads();
 }
 
-// Stages NB rows (row stride sb) into LDS unchanged.
-template <int NB>
-__device__ __forceinline__ void stage_plain(const f16* __restrict__ x, int64_t sb, int K,
-                                            f16* xs) {
-  const int C = K / 8;
-  for (int i = threadIdx.x; i < NB * C; i += kNT) {
-    const int b = i / C, c = i % C;
-    store16(xs + b * K + 8 * c, load16(x + b * sb + 8 * c));
+// Plain staging of NB rows (row stride sb, K = 8C) into LDS, likewise split:
+// thread t holds chunks t + kNT*i of the flattened (NB x C) chunk grid.
+template <int XP>
+__device__ __forceinline__ void plain_load(f16x8 (&v)[XP], const f16* __restrict__ x, int64_t sb,
+                                           int C, int NB) {
+  const int total = NB * C;
+#pragma unroll
+  for (int i = 0; i < XP; ++i) {
+    const int idx = min((int)threadIdx.x + kNT * i, total - 1);
+    const int b = idx / C, c = idx - b * C;
+    v[i] = load16(x + b * sb + 8 * c);
+  }
+}
+
+template <int XP>
+__device__ __forceinline__ void plain_finish(const f16x8 (&v)[XP], int C, int NB, f16* xs) {
+  const int total = NB * C;
+#pragma unroll
+  for (int i = 0; i < XP; ++i) {
+    const int idx = threadIdx.x + kNT * i;
+    if (idx < total) store16(xs + 8 * idx, v[i]);  // xs[b][c] at 8 * (b * C + c)
   }
   __syncthreads();
 }
@@ -191,22 +232,33 @@ __global__ __launch_bounds__(kNT) void rms_qkv_rope_append_kernel(QkvArgs a) {
   __shared__ float red[kNW * NB];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int K = a.K, C = K / 8;
-  const int p = blockIdx.x * kNW + w;
-  const bool valid = p < a.n_pairs;
+  const int p_raw = blockIdx.x * kNW + w;
+  const bool valid = p_raw < a.n_pairs;
+  const int p = valid ? p_raw : a.n_pairs - 1;  // spare waves load a real pair, store nothing
   const int head = p / (kHeadDim / 2), dd = p % (kHeadDim / 2);
   const int r0 = head * kHeadDim + dd, r1 = r0 + kHeadDim / 2;
 
-  f16x8 w0[NS], w1[NS];
-  if (valid) {
-    load_row<NS>(a.w + (int64_t)r0 * K, C, w0, lane);
-    load_row<NS>(a.w + (int64_t)r1 * K, C, w1, lane);
-  }
   const f16* rows[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b)
     rows[b] = a.x + (a.token != nullptr ? a.token[b] : (int64_t)b) * a.x_sb;
+  RmsStage<NB> st;
+  rms_load<NB>(st, rows, K, a.norm_w);
+  // Epilogue operands, loaded now so their latency hides under the weights':
+  // lane b < NB finishes batch row b.
+  const int be = lane < NB ? lane : 0;
+  const int64_t slot = a.write_index[0];
+  const float bias0 = a.bias != nullptr ? (float)a.bias[r0] : 0.f;
+  const float bias1 = a.bias != nullptr ? (float)a.bias[r1] : 0.f;
+  const f16* cp = a.cos + be * a.cs_sb;
+  const f16* sp = a.sin + be * a.cs_sb;
+  const float cos_lo = (float)cp[dd], sin_lo = (float)sp[dd];
+  const float cos_hi = (float)cp[dd + 32], sin_hi = (float)sp[dd + 32];
+  f16x8 w0[NS], w1[NS];
+  load_row<NS>(a.w + (int64_t)r0 * K, C, w0, lane);
+  load_row<NS>(a.w + (int64_t)r1 * K, C, w1, lane);
   f16* raw = (a.token != nullptr && blockIdx.x == 0) ? a.hidden_out : nullptr;
-  stage_rms<NB>(rows, K, a.norm_w, a.eps, xs, red, raw, a.ho_sb);
+  rms_finish<NB>(st, K, a.eps, xs, red, raw, a.ho_sb);
   if (!valid) return;
 
   float s0[NB], s1[NB];
@@ -226,16 +278,11 @@ __global__ __launch_bounds__(kNT) void rms_qkv_rope_append_kernel(QkvArgs a) {
 #pragma unroll
   for (int bb = 1; bb < NB; ++bb)
     if (b == bb) { v0 = s0[bb]; v1 = s1[bb]; }
-  const float bias0 = a.bias != nullptr ? (float)a.bias[r0] : 0.f;
-  const float bias1 = a.bias != nullptr ? (float)a.bias[r1] : 0.f;
   const float lo = (float)(f16)(v0 + bias0), hi = (float)(f16)(v1 + bias1);
-  const int64_t slot = a.write_index[0];
   const bool in_range = slot >= 0 && slot < a.cap;
   if (head < a.QH + a.KVH) {
-    const f16* cp = a.cos + b * a.cs_sb;
-    const f16* sp = a.sin + b * a.cs_sb;
     f16 olo, ohi;
-    rope1(lo, hi, (float)cp[dd], (float)sp[dd], (float)cp[dd + 32], (float)sp[dd + 32], olo, ohi);
+    rope1(lo, hi, cos_lo, sin_lo, cos_hi, sin_hi, olo, ohi);
     if (head < a.QH) {
       f16* q = a.q_out + b * a.qo_sb + head * a.qo_sh;
       q[dd] = olo;
@@ -263,24 +310,29 @@ struct GemvArgs {
 };
 
 // Each wave owns RW consecutive rows; hidden[b][n] = fp16(hidden + fp16(acc)).
-template <int NB, int NS, int RW>
+template <int NB, int NS, int RW, int XP>
 __global__ __launch_bounds__(kNT) void gemv_residual_kernel(GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) f16 xs_dyn[];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int K = a.K, C = K / 8;
   const int n0 = (blockIdx.x * kNW + w) * RW;
+  // Lane r*NB + b finishes (row n0 + r, batch row b); its residual is loaded now.
+  const int re = lane < RW * NB ? lane / NB : 0, be = lane < RW * NB ? lane % NB : 0;
+  f16* hp = a.hidden + be * a.h_sb + min(n0 + re, a.N - 1);
+  const float resid = (float)*hp;
+  f16x8 xv[XP];
+  plain_load<XP>(xv, a.inp, a.in_sb, C, NB);
   f16x8 wr[RW][NS];
 #pragma unroll
-  for (int r = 0; r < RW; ++r)
-    if (n0 + r < a.N) load_row<NS>(a.w + (int64_t)(n0 + r) * K, C, wr[r], lane);
-  stage_plain<NB>(a.inp, a.in_sb, K, xs_dyn);
+  for (int r = 0; r < RW; ++r) load_row<NS>(a.w + (int64_t)min(n0 + r, a.N - 1) * K, C, wr[r], lane);
+  plain_finish<XP>(xv, C, NB, xs_dyn);
   if (n0 >= a.N) return;
   float acc[RW][NB];
 #pragma unroll
   for (int r = 0; r < RW; ++r) {
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[r][b] = 0.f;
-    if (n0 + r < a.N) dot_row<NS, NB>(wr[r], xs_dyn, K, C, acc[r], lane);
+    dot_row<NS, NB>(wr[r], xs_dyn, K, C, acc[r], lane);
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[r][b] = wave_sum(acc[r][b]);
   }
@@ -293,10 +345,127 @@ __global__ __launch_bounds__(kNT) void gemv_residual_kernel(GemvArgs a) {
 #pragma unroll
     for (int bb = 0; bb < NB; ++bb)
       if (r == rr && b == bb) v = acc[rr][bb];
-  const int n = n0 + r;
-  if (n >= a.N) return;
-  f16* h = a.hidden + b * a.h_sb + n;
-  *h = (f16)((float)*h + (float)(f16)v);
+  if (n0 + r >= a.N) return;
+  *hp = (f16)(resid + (float)(f16)v);
+}
+
+// ---------------------------------------------------------------------------
+// o_proj with the split-K attention merge as its staging prologue.  Every
+// workgroup merges the decode kernel's partials (acc, m, l in the reference's
+// scratch layout, student_engine.py:117-162 algebra) for all B x KVH x G
+// query heads itself -- a few tens of KB of L2-resident reads -- instead of a
+// separate combine launch writing the fp16 attention output first.  The
+// merged row is rounded to fp16 exactly as the combine kernel rounds it
+// (out = fp16(A * (1 / L))), then hidden += fp16(att @ w_o^T).
+struct MergeArgs {
+  const float* acc;
+  const float* m;
+  const float* l;
+  int splits, KVH, G;
+  const f16* w;
+  f16* hidden;
+  int64_t h_sb;
+  int K, N;
+};
+
+template <int NB, int RW>
+__global__ __launch_bounds__(kNT) void attn_merge_gemv_residual_kernel(MergeArgs a) {
+  constexpr int NS = kMaxNormK / 8 / 64;
+  __shared__ __attribute__((aligned(16))) f16 xs[NB * kMaxNormK];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int K = a.K, C = K / 8;
+  const int n0 = (blockIdx.x * kNW + w) * RW;
+  const int re = lane < RW * NB ? lane / NB : 0, be = lane < RW * NB ? lane % NB : 0;
+  f16* hp = a.hidden + be * a.h_sb + min(n0 + re, a.N - 1);
+  const float resid = (float)*hp;
+  f16x8 wr[RW][NS];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) load_row<NS>(a.w + (int64_t)min(n0 + r, a.N - 1) * K, C, wr[r], lane);
+
+  // Merge: item = (b, h, g, 4 dims); xs offset of item `it` is 4 * it because
+  // hidden index (h * G + g) * 64 + d matches the (B, KVH, G, D) output layout.
+  // Thread t owns items t + kNT*i (i < NB covers NB * KVH * G * 16 <= NB * kNT
+  // items); each round loads four splits of every owned item at once.
+  const int S = a.splits, G = a.G;
+  const int items = NB * a.KVH * G * 16;
+  float M[NB], L[NB];
+  f32x4 A[NB];
+  int64_t ml0[NB], acc0[NB];  // split-0 index into m/l, and into acc as f32x4 slots
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int it = min((int)threadIdx.x + kNT * i, items - 1);
+    const int d4 = it & 15, bhg = it >> 4;
+    const int g = bhg % G, bh = bhg / G;
+    ml0[i] = (int64_t)bh * S * G + g;  // split s adds s * G
+    acc0[i] = ml0[i] * 16 + d4;        // split s adds s * G * 16
+    M[i] = kNegInf;
+    L[i] = 0.f;
+    A[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  for (int s0 = 0; s0 < S; s0 += 4) {
+    float mv[NB][4], lv[NB][4];
+    f32x4 av[NB][4];
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t off = (int64_t)min(s0 + u, S - 1) * G;
+        mv[i][u] = a.m[ml0[i] + off];
+        lv[i][u] = a.l[ml0[i] + off];
+        av[i][u] = reinterpret_cast<const f32x4*>(a.acc)[acc0[i] + off * 16];
+      }
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      float mc = M[i];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (s0 + u < S) mc = fmaxf(mc, mv[i][u]);
+      const float safe = (mc == kNegInf) ? 0.f : mc;
+      const float r = (M[i] == kNegInf) ? 0.f : fast_exp2((M[i] - safe) * kLog2e);
+      L[i] *= r;
+      A[i] *= r;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float wt = (s0 + u >= S || mv[i][u] == kNegInf) ? 0.f
+                                                               : fast_exp2((mv[i][u] - safe) * kLog2e);
+        L[i] += wt * lv[i][u];
+        A[i] += wt * av[i][u];
+      }
+      M[i] = mc;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const int it = threadIdx.x + kNT * i;
+    if (it < items) {
+      const float inv = 1.f / L[i];
+      f16x4 o;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) o[c] = (f16)(A[i][c] * inv);
+      *reinterpret_cast<f16x4*>(xs + 4 * it) = o;
+    }
+  }
+  __syncthreads();
+  if (n0 >= a.N) return;
+  float acc[RW][NB];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[r][b] = 0.f;
+    dot_row<NS, NB>(wr[r], xs, K, C, acc[r], lane);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[r][b] = wave_sum(acc[r][b]);
+  }
+  if (lane >= RW * NB) return;
+  const int r = lane / NB, b = lane % NB;
+  float v = acc[0][0];
+#pragma unroll
+  for (int rr = 0; rr < RW; ++rr)
+#pragma unroll
+    for (int bb = 0; bb < NB; ++bb)
+      if (r == rr && b == bb) v = acc[rr][bb];
+  if (n0 + r >= a.N) return;
+  *hp = (f16)(resid + (float)(f16)v);
 }
 
 // ---------------------------------------------------------------------------
@@ -320,28 +489,27 @@ __global__ __launch_bounds__(kNT) void rms_gate_up_swiglu_kernel(GateUpArgs a) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int K = a.K, C = K / 8;
   const int j0 = (blockIdx.x * kNW + w) * PW;
-  f16x8 wg[PW][NS], wu[PW][NS];
-#pragma unroll
-  for (int pp = 0; pp < PW; ++pp) {
-    if (j0 + pp < a.I) {
-      load_row<NS>(a.w + (int64_t)(j0 + pp) * K, C, wg[pp], lane);
-      load_row<NS>(a.w + (int64_t)(a.I + j0 + pp) * K, C, wu[pp], lane);
-    }
-  }
   const f16* rows[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) rows[b] = a.x + b * a.x_sb;
-  stage_rms<NB>(rows, K, a.norm_w, a.eps, xs, red, nullptr, 0);
+  RmsStage<NB> st;
+  rms_load<NB>(st, rows, K, a.norm_w);
+  f16x8 wg[PW][NS], wu[PW][NS];
+#pragma unroll
+  for (int pp = 0; pp < PW; ++pp) {
+    const int j = min(j0 + pp, a.I - 1);
+    load_row<NS>(a.w + (int64_t)j * K, C, wg[pp], lane);
+    load_row<NS>(a.w + (int64_t)(a.I + j) * K, C, wu[pp], lane);
+  }
+  rms_finish<NB>(st, K, a.eps, xs, red, nullptr, 0);
   if (j0 >= a.I) return;
   float ag[PW][NB], au[PW][NB];
 #pragma unroll
   for (int pp = 0; pp < PW; ++pp) {
 #pragma unroll
     for (int b = 0; b < NB; ++b) ag[pp][b] = au[pp][b] = 0.f;
-    if (j0 + pp < a.I) {
-      dot_row<NS, NB>(wg[pp], xs, K, C, ag[pp], lane);
-      dot_row<NS, NB>(wu[pp], xs, K, C, au[pp], lane);
-    }
+    dot_row<NS, NB>(wg[pp], xs, K, C, ag[pp], lane);
+    dot_row<NS, NB>(wu[pp], xs, K, C, au[pp], lane);
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       ag[pp][b] = wave_sum(ag[pp][b]);
@@ -403,26 +571,22 @@ __global__ __launch_bounds__(kNT) void rms_lm_head_kernel(LmArgs a) {
   f16x8 cur[RW][NS], nxt[RW][NS];
   auto load_group = [&](int grp, f16x8 (&buf)[RW][NS]) {
 #pragma unroll
-    for (int r = 0; r < RW; ++r) {
-      const int n = grp * RW + r;
-      if (n < a.V) load_row<NS>(a.w + (int64_t)n * K, C, buf[r], lane);
-      else {
-#pragma unroll
-        for (int s = 0; s < NS; ++s) buf[r][s] = zero8();
-      }
-    }
+    for (int r = 0; r < RW; ++r)
+      load_row<NS>(a.w + (int64_t)min(grp * RW + r, a.V - 1) * K, C, buf[r], lane);
   };
-  if (g < groups) load_group(g, cur);
   const f16* rows[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) rows[b] = a.x + b * a.x_sb;
-  stage_rms<NB>(rows, K, a.norm_w, a.eps, xs, red, nullptr, 0);
+  RmsStage<NB> st;
+  rms_load<NB>(st, rows, K, a.norm_w);
+  load_group(min(g, groups - 1), cur);
+  rms_finish<NB>(st, K, a.eps, xs, red, nullptr, 0);
 
   uint64_t best[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) best[b] = 0;
   for (; g < groups; g += stride) {
-    if (g + stride < groups) load_group(g + stride, nxt);
+    load_group(min(g + stride, groups - 1), nxt);  // past the end: a real row, unused
     float acc[RW][NB];
 #pragma unroll
     for (int r = 0; r < RW; ++r) {
@@ -478,36 +642,46 @@ struct FinArgs {
 };
 
 __global__ __launch_bounds__(256) void argmax_step_kernel(FinArgs a) {
-  __shared__ uint64_t part[256];
-  __shared__ int64_t chosen[kMaxB];
-  for (int b = 0; b < a.B; ++b) {
-    uint64_t k = 0;
-    for (int j = threadIdx.x; j < a.n_blocks; j += 256) {
-      const uint64_t v = a.keys[(int64_t)b * a.n_blocks + j];
-      k = v > k ? v : k;
-    }
-    part[threadIdx.x] = k;
-    __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) {
-      if (threadIdx.x < o) {
-        const uint64_t v = part[threadIdx.x + o];
-        if (v > part[threadIdx.x]) part[threadIdx.x] = v;
-      }
-      __syncthreads();
-    }
-    if (threadIdx.x == 0) chosen[b] = (int64_t)(0xFFFFFFFFu - (unsigned)(part[0] & 0xFFFFFFFFu));
-    __syncthreads();
-  }
-  if (threadIdx.x != 0) return;
+  __shared__ uint64_t part[kMaxB][256];
+  const int tid = threadIdx.x;
+  // Every load is issued before any wait: the keys, the step counter and
+  // (thread b) row b's position.
   const int64_t s = a.step != nullptr ? a.step[0] : 0;
-  for (int b = 0; b < a.B; ++b) {
-    a.token[b] = chosen[b];
-    if (a.rows != nullptr && a.step != nullptr && s >= 0 && s < a.n_rows)
-      a.rows[b * a.rows_sb + s] = chosen[b];
-    if (a.pos != nullptr) a.pos[b] += 1;
+  const int64_t p = (a.pos != nullptr && tid < a.B) ? a.pos[tid] : 0;
+  const int64_t wi = (a.write_index != nullptr && tid == 0) ? a.write_index[0] : 0;
+  uint64_t k[kMaxB];
+#pragma unroll
+  for (int b = 0; b < kMaxB; ++b) {
+    k[b] = 0;
+    if (b < a.B) {
+      for (int j = tid; j < a.n_blocks; j += 256) {
+        const uint64_t v = a.keys[(int64_t)b * a.n_blocks + j];
+        k[b] = v > k[b] ? v : k[b];
+      }
+    }
+    part[b][tid] = k[b];
   }
-  if (a.write_index != nullptr) a.write_index[0] += 1;
-  if (a.step != nullptr) a.step[0] = s + 1;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
+    if (tid < o) {
+#pragma unroll
+      for (int b = 0; b < kMaxB; ++b) {
+        const uint64_t v = part[b][tid + o];
+        if (v > part[b][tid]) part[b][tid] = v;
+      }
+    }
+    __syncthreads();
+  }
+  if (tid < a.B) {
+    const int64_t tok = (int64_t)(0xFFFFFFFFu - (unsigned)(part[tid][0] & 0xFFFFFFFFu));
+    a.token[tid] = tok;
+    if (a.rows != nullptr && s >= 0 && s < a.n_rows) a.rows[tid * a.rows_sb + s] = tok;
+    if (a.pos != nullptr) a.pos[tid] = p + 1;
+  }
+  if (tid == 0) {
+    if (a.write_index != nullptr) a.write_index[0] = wi + 1;
+    if (a.step != nullptr) a.step[0] = s + 1;
+  }
 }
 
 }  // namespace step
@@ -580,14 +754,43 @@ extern "C" int qf_gemv_residual(const void* inp, int64_t in_sb, const void* w, v
   const dim3 block(kNT);
   const int C = K / 8;
   if (C <= 128) {
-    // Short rows (o_proj): two rows per wave.
+    // Short rows (o_proj): two rows per wave; the B x K input is at most two
+    // chunks per thread.
     const dim3 grid((N + kNW * 2 - 1) / (kNW * 2));
-    QF_DISPATCH_B(B, gemv_residual_kernel, 2, 2)
+    if (B * C <= kNT) { QF_DISPATCH_B(B, gemv_residual_kernel, 2, 2, 1) }
+    else { QF_DISPATCH_B(B, gemv_residual_kernel, 2, 2, 2) }
   } else {
     // Long rows (down_proj): one row per wave, the whole row in flight.
     const dim3 grid((N + kNW - 1) / kNW);
-    QF_DISPATCH_B(B, gemv_residual_kernel, 16, 1)
+    if (B * C <= 4 * kNT) { QF_DISPATCH_B(B, gemv_residual_kernel, 16, 1, 4) }
+    else if (B * C <= 8 * kNT) { QF_DISPATCH_B(B, gemv_residual_kernel, 16, 1, 8) }
+    else { QF_DISPATCH_B(B, gemv_residual_kernel, 16, 1, 16) }
   }
+  return (int)hipGetLastError();
+}
+
+extern "C" int qf_attn_merge_o_proj(const float* acc, const float* m, const float* l, int splits,
+                                    int KVH, int G, const void* w_o, void* hidden, int64_t h_sb,
+                                    int B, int N, void* stream) {
+  const int K = KVH * G * kHeadDim;
+  if (B < 1 || B > kMaxB || G < 1 || KVH < 1 || K > kMaxNormK || KVH * G * 16 > kNT)
+    return QF_ERR_UNSUPPORTED;
+  if (!acc || !m || !l || !w_o || !hidden || N < 1 || splits < 1) return QF_ERR_INVALID_ARG;
+  if (!al16(acc) || !al16(w_o)) return QF_ERR_INVALID_ARG;
+  MergeArgs a;
+  a.acc = acc; a.m = m; a.l = l;
+  a.splits = splits; a.KVH = KVH; a.G = G;
+  a.w = static_cast<const f16*>(w_o);
+  a.hidden = static_cast<f16*>(hidden); a.h_sb = h_sb;
+  a.K = K; a.N = N;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  // Every workgroup re-reads all partials, so batched calls use fewer, wider
+  // workgroups (measured on MI355X: B=1 best at 2 rows per wave, B=4 at 4).
+  const int RW = B == 1 ? 2 : 4;
+  const dim3 grid((N + kNW * RW - 1) / (kNW * RW)), block(kNT);
+  const size_t shm = 0;
+  if (RW == 2) { QF_DISPATCH_B(B, attn_merge_gemv_residual_kernel, 2) }
+  else { QF_DISPATCH_B(B, attn_merge_gemv_residual_kernel, 4) }
   return (int)hipGetLastError();
 }
 

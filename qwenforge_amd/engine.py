@@ -17,10 +17,10 @@ Mirrors the reference's cached generation path without the tokenizer:
 
 For batches of 1..4 rows the decode step body is the fused weight-streaming
 path (``step_ops``, include/qf_step.h): per layer one launch for rms_norm +
-QKV + RoPE + append, the attention launch(es), one for o_proj + residual, one
-for rms_norm + gate/up + SwiGLU and one for down_proj + residual; then one
-for rms_norm + lm_head + per-block argmax and one for the argmax and the slot
-bookkeeping.  Larger batches keep the torch projections (hipBLASLt / ATen
+QKV + RoPE + append, the split-K attention launch, one for the split merge +
+o_proj + residual, one for rms_norm + gate/up + SwiGLU and one for down_proj +
+residual; then one for rms_norm + lm_head + per-block argmax and one for the
+argmax and the slot bookkeeping.  Larger batches keep the torch projections (hipBLASLt / ATen
 kernels) around the same HIP attention kernels.  Prefill always uses the torch
 projections.  Everything is fp16 storage with the reference's rounding points.
 """
@@ -127,9 +127,10 @@ class DecodeEngine:
                                              layer["qkv_bias"], cos, sin, kc, vc, ctx["write"],
                                              q_rot)
             grouped = q_rot.view(b, cfg.kv_heads, cfg.groups, cfg.head_dim)
-            att = ops.flash_decode_attention(grouped, kc, vc, ctx["bias"], ctx["flash"],
-                                             kv_last=ctx["write"], scale=self.scale)
-            step_ops.gemv_residual(att.view(b, cfg.hidden), layer["o_weight"], hidden)
+            # Split-K partials; their merge is the o_proj kernel's prologue.
+            ops.flash_decode_split(grouped, kc, vc, ctx["bias"], ctx["flash"],
+                                   kv_last=ctx["write"], scale=self.scale)
+            step_ops.attn_merge_o_proj(ctx["flash"], layer["o_weight"], hidden)
             step_ops.rms_gate_up_swiglu(hidden, layer["post_norm"], eps, layer["gate_up_weight"], h)
             step_ops.gemv_residual(h, layer["down_weight"], hidden)
         step_ops.rms_lm_head(hidden, self.w["final_norm"], eps, self.w["lm_head"], ctx["logits"],
@@ -166,6 +167,21 @@ class DecodeEngine:
         ctx["pos"].add_(1)
         ctx["step"].add_(1)
 
+    @staticmethod
+    def fused_max_splits(batch: int) -> int:
+        """Split cap of the fused step.  Every o_proj workgroup merges all splits
+        of all rows, so that prologue's traffic grows with splits x rows;
+        measured on MI355X at Qwen2.5-0.5B shape: 8 splits at B=1, 4 above."""
+        return 8 if batch == 1 else 4
+
+    def _flash_scratch(self, batch: int, cap: int):
+        cfg = self.cfg
+        if not self.uses_fused_step(batch):
+            return ops.make_flash_scratch(batch, cfg.kv_heads, cfg.groups, cap, self.device)
+        splits = min(ops.choose_splits(batch, cfg.kv_heads, cap), self.fused_max_splits(batch))
+        return ops.make_flash_scratch(batch, cfg.kv_heads, cfg.groups, cap, self.device,
+                                      splits=splits, fused=False)
+
     def make_context(self, caches, batch: int, max_new_tokens: int, bias_mask=None):
         """Static buffers of the graph step.  ``bias_mask`` (B, cap) bool marks
         valid prompt slots when rows are right-padded; None means no holes, so
@@ -181,7 +197,7 @@ class DecodeEngine:
         ctx = {
             "caches": caches,
             "bias": bias,
-            "flash": ops.make_flash_scratch(batch, cfg.kv_heads, cfg.groups, cap, dev),
+            "flash": self._flash_scratch(batch, cap),
             "token": torch.zeros(batch, device=dev, dtype=torch.long),
             "pos": torch.zeros(batch, device=dev, dtype=torch.long),
             "write": torch.zeros(1, device=dev, dtype=torch.long),

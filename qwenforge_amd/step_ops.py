@@ -8,6 +8,8 @@ They replace the torch op sequence inside the reference's graph step
   of ``token`` first (SE:896).
 * ``gemv_residual`` -- ``hidden = residual + F.linear(inp, w)`` in place
   (o_proj SE:973-974, down_proj SE:978 / SE:666).
+* ``attn_merge_o_proj`` -- the split-K decode merge (SE:117-162) folded into
+  the o_proj + residual GEMV.
 * ``rms_gate_up_swiglu`` -- rms_norm + gate/up linear + ``silu(gate) * up``
   (SE:976-977, SE:664-666).
 * ``rms_lm_head`` + ``argmax_step`` -- final rms_norm, lm_head, argmax
@@ -132,6 +134,31 @@ def gemv_residual(inp: torch.Tensor, w: torch.Tensor, hidden: torch.Tensor) -> N
     rc = _lib.load().qf_gemv_residual(inp.data_ptr(), in_sb, w.data_ptr(), hidden.data_ptr(),
                                       h_sb, b, k, n, _stream(inp.device))
     _lib.check(rc, "qf_gemv_residual")
+
+
+def attn_merge_o_proj(flash, w_o: torch.Tensor, hidden: torch.Tensor) -> None:
+    """hidden <- fp16(hidden + fp16(merge(flash partials) @ w_o^T)), in place.
+
+    ``flash`` is the decode scratch filled by ``ops.flash_decode_split``:
+    acc (B, KVH, S, G, 64), m and l (B, KVH, S, G), fp32 contiguous.  The
+    merge replaces the combine launch (SE:117-162); see include/qf_step.h.
+    """
+    acc, m, l = flash[:3]
+    b, kvh, splits, g, d = acc.shape
+    _batch(b)
+    for name, t in (("acc", acc), ("m", m), ("l", l)):
+        _check(name, t, torch.float32)
+        if not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+    if d != HEAD_DIM or m.shape != (b, kvh, splits, g) or l.shape != m.shape:
+        raise ValueError("flash partials must be (B, KVH, S, G, 64) / (B, KVH, S, G)")
+    n = w_o.shape[0]
+    _weight("w_o", w_o, n, kvh * g * d)
+    h_sb = _rows("hidden", hidden, b, n)
+    rc = _lib.load().qf_attn_merge_o_proj(acc.data_ptr(), m.data_ptr(), l.data_ptr(), splits,
+                                          kvh, g, w_o.data_ptr(), hidden.data_ptr(), h_sb, b, n,
+                                          _stream(hidden.device))
+    _lib.check(rc, "qf_attn_merge_o_proj")
 
 
 def rms_gate_up_swiglu(x: torch.Tensor, norm_w: torch.Tensor, eps: float, w_gate_up: torch.Tensor,

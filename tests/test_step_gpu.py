@@ -209,3 +209,36 @@ def test_lm_head_random_logits_close(dev):
     assert ok, err
     # The device argmax is the first maximum of the device logits.
     assert torch.equal(token.cpu(), logits.float().cpu().argmax(-1))
+
+
+@pytest.mark.parametrize("batch", [1, 4])
+@pytest.mark.parametrize("splits", [1, 5, 18])
+def test_attn_merge_o_proj(dev, batch, splits):
+    """Split-K partials merged in the o_proj prologue == oracle attention + o_proj."""
+    import oracle
+    from qwenforge_amd import ops, workloads
+
+    gen = torch.Generator().manual_seed(40 + batch + splits)
+    case = workloads.decode_uniform(batch, 700, seed=splits, cap=768)
+    c = case.to(dev)
+    flash = ops.make_flash_scratch(batch, KVH, QH // KVH, 768, dev, splits=splits, fused=False)
+    kv_last = torch.tensor([699], device=dev)
+    w_o = _rand(HIDDEN, HIDDEN, gen=gen, std=0.02)
+    res = _rand(batch, HIDDEN, gen=gen)
+    hidden = res.to(dev)
+    print(f"[merge+o_proj] B={batch} S={splits}", flush=True)
+    ops.flash_decode_split(c.grouped, c.key_cache, c.value_cache, None, flash, kv_last=kv_last)
+    step_ops.attn_merge_o_proj(flash, w_o.to(dev), hidden)
+    # The unfused pair: combine launch, then the plain GEMV.
+    out = ops.flash_decode_combine(flash)
+    hidden2 = res.to(dev)
+    step_ops.gemv_residual(out.view(batch, HIDDEN), w_o.to(dev), hidden2)
+    torch.cuda.synchronize()
+    bias = torch.full((batch, 768), float(torch.finfo(torch.float16).min))
+    bias[:, :700] = 0
+    att = oracle.grouped_decode_attention(case.grouped, case.key_cache, case.value_cache, bias)
+    ref = ost.residual16(res, att.to(torch.float16).reshape(batch, HIDDEN), w_o)
+    ok, err = _close(hidden, ref)
+    assert ok, err
+    ok, err = _close(hidden, hidden2.cpu(), tol=2e-3)
+    assert ok, err
