@@ -63,7 +63,7 @@ struct DecodeArgs {
   f16* out;
   int64_t o_sb, o_sh, o_sg;
   int B, KVH, G, cap, splits;
-  int bias_vec;      // bias rows are 16-byte aligned: 8 keys per load
+  int bias_vec;      // bias rows 16-byte aligned and cap % 8 == 0: 8 keys per load
   float scale_log2;  // scale * log2(e)
 };
 
@@ -190,13 +190,24 @@ __device__ void merge_parts(const DecodeArgs& a, int bh, int q0, int nq, int fir
   }
 }
 
+enum Bias { kNoBias = 0, kBiasVec = 1, kBiasScalar = 2 };
+
 struct Tile {
   f16x8 k[2][2];  // [score block j][k step kk]
   f16x8 v[4];     // 4 keys x 8 dims
+  f16x8 bias;     // bias of the lane's keys t0 + 8*grp .. +7
 };
 
-__device__ __forceinline__ void load_tile(Tile& t, const f16* kb, const f16* vb, int64_t k_sn,
-                                          int64_t v_sn, int t0, int last, int lane) {
+// Issues every load of one 32-key tile -- K operands, V rows and the bias of
+// the lane's 8 keys -- with no wait in between.  Keys past `last` re-read
+// slot `last` (their scores are masked).  kBiasVec reads the 8 bias values
+// as one 16-byte load from min(kbase, cap - 8): in bounds, aligned (the
+// caller checks cap % 8 == 0 and 16-byte rows), and correct for every key
+// below cap because kbase is a multiple of 8.
+template <int kBias>
+__device__ __forceinline__ void load_tile(Tile& t, const f16* kb, const f16* vb, const f16* biasb,
+                                          int64_t k_sn, int64_t v_sn, int t0, int last, int cap,
+                                          int lane) {
   const int col = lane & 15, grp = lane >> 4;
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -216,10 +227,18 @@ __device__ __forceinline__ void load_tile(Tile& t, const f16* kb, const f16* vb,
     key = key < last ? key : last;
     t.v[r] = load16(vb + (int64_t)key * v_sn + c8);
   }
+  const int kbase = t0 + 8 * grp;
+  if (kBias == kBiasVec) {
+    t.bias = load16(biasb + (kbase < cap - 8 ? kbase : cap - 8));
+  } else if (kBias == kBiasScalar) {
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj) t.bias[jj] = biasb[kbase + jj < last ? kbase + jj : last];
+  }
 }
 
-template <int NW, bool kHasBias, int kMode>
+template <int NW, int kBias, int kMode>
 __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
+  constexpr bool kHasBias = kBias != kNoBias;
   constexpr int NT = NW * 64;
   constexpr bool kCoh = kMode == kFused;
   // LDS: per-wave transposed V tiles during the sweep, reused for the
@@ -241,23 +260,26 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
   const int col = lane & 15;  // query column / A-operand row
   const int grp = lane >> 4;  // 8-wide k chunk of the operands
 
-  int lo, hi;
-  split_range(a, b, s, lo, hi);
-
-  // Q^T operand: lane holds Q[col][32*kk + 8*grp .. +7].
+  // Q^T operand: lane holds Q[col][32*kk + 8*grp .. +7].  Issued before the
+  // split range is known (it may depend on kv_last, a device load).
+  // Columns >= G load query G-1 (in bounds) and are zeroed by a select, so
+  // the loads carry no branch and fly together with the first tile's.
   f16x8 qf[2];
   {
-    const f16* qp = a.q + b * a.q_sb + h * a.q_sh + col * a.q_sg + 8 * grp;
+    const int qc = col < a.G ? col : a.G - 1;
+    const f16* qp = a.q + b * a.q_sb + h * a.q_sh + qc * a.q_sg + 8 * grp;
+    f16x8 zero;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) zero[e] = (f16)0.f;
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
-      if (col < a.G) {
-        qf[kk] = load16(qp + 32 * kk);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qf[kk][e] = (f16)0.f;
-      }
+      const f16x8 ld = load16(qp + 32 * kk);
+      qf[kk] = col < a.G ? ld : zero;
     }
   }
+
+  int lo, hi;
+  split_range(a, b, s, lo, hi);
 
   float m_run = kNegInf, l_run = 0.f;
   f32x4 o[4];
@@ -272,26 +294,17 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
 
   int t0 = lo + w * kTile;
   Tile cur, nxt;
-  if (t0 < hi) load_tile(cur, kb, vb, a.k_sn, a.v_sn, t0, last, lane);
+  if (t0 < hi) load_tile<kBias>(cur, kb, vb, biasb, a.k_sn, a.v_sn, t0, last, a.cap, lane);
   for (; t0 < hi; t0 += NW * kTile) {
     const int tn = t0 + NW * kTile;
-    if (tn < hi) load_tile(nxt, kb, vb, a.k_sn, a.v_sn, tn, last, lane);
+    if (tn < hi) load_tile<kBias>(nxt, kb, vb, biasb, a.k_sn, a.v_sn, tn, last, a.cap, lane);
 
-    // Bias of the lane's 8 keys t0 + 8*grp + jj.
+    // Bias of the lane's 8 keys t0 + 8*grp + jj, in log2 units.
     float bv[8];
     const int kbase = t0 + 8 * grp;
     if (kHasBias) {
-      if (a.bias_vec && kbase + 7 <= last) {
-        const f16x8 b8 = load16(biasb + kbase);
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj) bv[jj] = (float)b8[jj] * kLog2e;
-      } else {
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-          const int kc = kbase + jj < last ? kbase + jj : last;
-          bv[jj] = (float)biasb[kc] * kLog2e;
-        }
-      }
+      for (int jj = 0; jj < 8; ++jj) bv[jj] = (float)cur.bias[jj] * kLog2e;
     }
 
     f32x4 c0 = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
@@ -429,18 +442,19 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
   merge_parts<256, false>(a, bh, q, 1, 0, 1, a.splits, true, lds);
 }
 
-template <int NW, bool kHasBias>
+template <int NW, int kBias>
 static void launch_split(const DecodeArgs& a, int mode, dim3 grid, hipStream_t st) {
   const dim3 block(NW * 64);
-  if (mode == kDirect) hipLaunchKernelGGL((decode_split_kernel<NW, kHasBias, kDirect>), grid, block, 0, st, a);
-  else if (mode == kPartial) hipLaunchKernelGGL((decode_split_kernel<NW, kHasBias, kPartial>), grid, block, 0, st, a);
-  else hipLaunchKernelGGL((decode_split_kernel<NW, kHasBias, kFused>), grid, block, 0, st, a);
+  if (mode == kDirect) hipLaunchKernelGGL((decode_split_kernel<NW, kBias, kDirect>), grid, block, 0, st, a);
+  else if (mode == kPartial) hipLaunchKernelGGL((decode_split_kernel<NW, kBias, kPartial>), grid, block, 0, st, a);
+  else hipLaunchKernelGGL((decode_split_kernel<NW, kBias, kFused>), grid, block, 0, st, a);
 }
 
 template <int NW>
 static void launch_nw(const DecodeArgs& a, int mode, dim3 grid, hipStream_t st) {
-  if (a.bias) launch_split<NW, true>(a, mode, grid, st);
-  else launch_split<NW, false>(a, mode, grid, st);
+  if (!a.bias) launch_split<NW, kNoBias>(a, mode, grid, st);
+  else if (a.bias_vec) launch_split<NW, kBiasVec>(a, mode, grid, st);
+  else launch_split<NW, kBiasScalar>(a, mode, grid, st);
 }
 
 }  // namespace qf
@@ -492,7 +506,7 @@ static int make_args(DecodeArgs& a, const void* q, int64_t q_sb, int64_t q_sh, i
   a.v_sb = v_sb; a.v_sh = v_sh; a.v_sn = v_sn;
   a.bias = static_cast<const f16*>(bias);
   a.bias_sb = bias_sb;
-  a.bias_vec = bias != nullptr && aligned16(bias) && (bias_sb & 7) == 0;
+  a.bias_vec = bias != nullptr && aligned16(bias) && (bias_sb & 7) == 0 && cap % 8 == 0 && cap >= 8;
   a.kv_last = kv_last;
   a.kv_last_sb = kv_last_sb;
   a.acc = acc; a.m = m; a.l = l;
