@@ -162,6 +162,40 @@ def bench_long_decode(steps, warmup, dev):
     return dict(us_per_layer=ms * 1e3, bytes=base.valid_bytes, splits=splits)
 
 
+def bench_bandwidth_decode(steps, warmup, dev, batch, length):
+    """Decode attention where K/V streaming dominates (the >= 60%-of-HBM regime,
+    KV length >= 4096): B x L slots per kv head, no bias, caches rotated so the
+    set is at least twice the MALL.  Returns the full call (split + merge)
+    and the split kernel alone, per layer."""
+    import torch
+
+    from qwenforge_amd import ops, workloads
+
+    base = workloads.decode_uniform(batch, length, seed=1)
+    per = base.key_cache.numel() * 2 * 2
+    reps = max(2, -(-2 * MALL_BYTES // per))
+    q = base.grouped.to(dev)
+    k0, v0 = base.key_cache.to(dev), base.value_cache.to(dev)
+    ks = [k0] + [k0.clone() for _ in range(reps - 1)]
+    vs = [v0] + [v0.clone() for _ in range(reps - 1)]
+    splits = ops.choose_splits(batch, 2, length)
+    flash = ops.make_flash_scratch(batch, 2, 7, length, dev, splits=splits)
+
+    def full():
+        for r in range(reps):
+            ops.flash_decode_attention(q, ks[r], vs[r], None, flash)
+
+    def split_only():
+        for r in range(reps):
+            ops.flash_decode_split(q, ks[r], vs[r], None, flash[:4])
+
+    ms_full = _time_graphs([GraphStep(full)], max(1, steps // 4), max(1, warmup // 4)) / reps
+    ms_split = _time_graphs([GraphStep(split_only)], max(1, steps // 4), max(1, warmup // 4)) / reps
+    nbytes = base.valid_bytes
+    return dict(batch=batch, length=length, splits=splits, fused=len(flash) > 4,
+                us_full=ms_full * 1e3, us_split=ms_split * 1e3, bytes=nbytes)
+
+
 def bench_prefill(steps, warmup, dev):
     """Config 4: causal prefill S=2048 with fused RoPE + cache append."""
     import torch
@@ -344,6 +378,21 @@ def main():
             "hbm_frac": round(lg["bytes"] / (lg["us_per_layer"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "splits": lg["splits"],
         }
+        bw = {}
+        for b, L in ((16, 32768), (64, 4096)):
+            x = bench_bandwidth_decode(args.steps, args.warmup, dev, b, L)
+            gbs_full = x["bytes"] / (x["us_full"] * 1e-6) / 1e9
+            gbs_split = x["bytes"] / (x["us_split"] * 1e-6) / 1e9
+            bw[f"B{b}_L{L}"] = {
+                "us_per_layer": round(x["us_full"], 3),
+                "GBps": round(gbs_full, 1),
+                "hbm_frac": round(gbs_full / HBM_PEAK_GBS, 4),
+                "split_kernel_us": round(x["us_split"], 3),
+                "split_kernel_hbm_frac": round(gbs_split / HBM_PEAK_GBS, 4),
+                "splits": x["splits"],
+                "merge": "fused single launch" if x["fused"] else "split + combine launches",
+            }
+        line["bandwidth_decode"] = bw
         pf = bench_prefill(args.steps, args.warmup, dev)
         tf = pf["flops"] / (pf["us_per_layer"] * 1e-6) / 1e12
         line["prefill_cfg4"] = {
