@@ -144,6 +144,33 @@ int qf_prefill_attn(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sn,
                     void* stream);
 
 /*
+ * qf_prefill_attn with a caller-owned workspace that lets the heaviest query
+ * tiles split their key range over two workgroups (the causal prefill's
+ * longest chain is the last query tile's; split, it halves).  The split
+ * query tiles write fp32 partials to `workspace` and a second launch merges
+ * them into `out`; the result is the same attention up to fp32 summation
+ * order.  workspace == NULL (or workspace_bytes == 0) is qf_prefill_attn.
+ * A non-NULL workspace must be 16-byte aligned and at least
+ * qf_prefill_workspace_bytes(B, QH, S) bytes, else QF_ERR_INVALID_ARG.
+ * No counterpart in the reference (its Triton kernel has one program per
+ * query tile, SE:276-280); the op wrapper allocates the workspace.
+ */
+int qf_prefill_attn_ws(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sn,
+                       const void* k, int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                       const void* v, int64_t v_sb, int64_t v_sh, int64_t v_sn,
+                       const void* cos, const void* sin, int64_t cs_sb, int64_t cs_sn,
+                       void* k_cache, int64_t kc_sb, int64_t kc_sh, int64_t kc_sn,
+                       void* v_cache, int64_t vc_sb, int64_t vc_sh, int64_t vc_sn,
+                       int64_t start_pos, int cap,
+                       void* out, int64_t o_sb, int64_t o_sh, int64_t o_sn,
+                       int B, int QH, int KVH, int S, int D, float scale,
+                       void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes qf_prefill_attn_ws uses for (B, QH, S); 0 when the shape
+ * gains nothing from splitting (short prompts). */
+int64_t qf_prefill_workspace_bytes(int B, int QH, int S);
+
+/*
  * One-token RoPE + KV-cache append (decode).
  *
  * Replaces the eager RoPE of the graph step (student_engine.py:927-928, with

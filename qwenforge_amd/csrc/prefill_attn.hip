@@ -60,6 +60,12 @@ struct Args {
   int64_t o_sb, o_sh, o_sn;
   int B, QH, KVH, G, S;
   float scale_log2;
+  // Split-K of the heaviest query tiles (LDS kernel only): query tiles
+  // mt >= split_from run as two workgroups over key tiles [0, split_from) and
+  // [split_from, mt], which write fp32 partials to `part` for the merge
+  // kernel.  n_split = number of split query tiles (0: no split).
+  float* part;
+  int split_from, n_split;
 };
 
 // Registers holding one K/V tile between its global load and its LDS store.
@@ -338,6 +344,7 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(Args a) {
 // that address 4 keys x 16 dims of V receive V^T[d][4 keys] directly.
 constexpr int kStages = 3;
 constexpr int kRowBytes = kD * 2;  // 128
+constexpr int kPartVals = kD + 2;  // per query row of a split partial: o[64], m, l
 
 __device__ __forceinline__ int swz(int row) { return 2 * ((row >> 3) & 3) + ((row >> 1) & 1); }
 
@@ -361,8 +368,8 @@ __device__ __forceinline__ f16x4 ds_read_tr16(const unsigned char* p) {
 struct LdsCtx {
   const f16* kb;
   const f16* vb;
-  const f16* kp[2];   // tile-0 source of this lane's two K rows (row lrow0 + 8i, its chunk)
-  const f16* vp[2];   // same for V
+  int kvo[2];         // byte offset, within a tile, of this lane's two K rows' chunk
+  int vvo[2];         // same for V
   int64_t k_sn, v_sn;
   int S, mt, qrow, n_ktiles, grp, lrow0, pch, w;
   int koff[2][2][2];  // [ch][j][kk] LDS byte offsets of the K operand reads
@@ -373,29 +380,51 @@ struct LdsCtx {
   f32x4 o[4];
 };
 
+// Buffer resource over the rows [key0, S) of a K or V head (row stride sn
+// elements): the tile's base address and valid byte count live in SGPRs, so
+// a lane's load offset within the tile never changes, and rows past the
+// sequence (the last tile's tail) read as zero (their scores are masked).
+// Needs sn >= 64 so the last row's 128 bytes lie below the record count.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const f16* head, int64_t sn, int key0,
+                                                            int S) {
+  const int64_t bytes = (int64_t)(S - key0) * sn * 2;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(head + key0 * sn), (short)0,
+                                           (int)(bytes < 0x7fffffff ? bytes : 0x7fffffff),
+                                           0x00020000);
+}
+
 // Async loads of tile kt (this wave's 16 rows of K and of V) into (Kd, Vd).
 __device__ __forceinline__ void lds_issue(const LdsCtx& c, int kt, unsigned char* Kd,
                                           unsigned char* Vd) {
   const int key0 = kt * kBN;
-  const bool tail = key0 + kBN > c.S;
+  const __amdgpu_buffer_rsrc_t rk = tile_rsrc(c.kb, c.k_sn, key0, c.S);
+  const __amdgpu_buffer_rsrc_t rv = tile_rsrc(c.vb, c.v_sn, key0, c.S);
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const f16* ks;
-    const f16* vs;
-    if (!tail) {  // uniform: whole tile inside the sequence, pointer + scalar offset
-      ks = c.kp[i] + key0 * c.k_sn;
-      vs = c.vp[i] + key0 * c.v_sn;
-    } else {      // last tile: rows past the sequence repeat row S-1 (masked later)
-      const int r = c.lrow0 + 8 * i;
-      const int ch = c.pch ^ swz(r);
-      int key = key0 + r;
-      key = key < c.S ? key : c.S - 1;
-      ks = c.kb + (int64_t)key * c.k_sn + 8 * ch;
-      vs = c.vb + (int64_t)key * c.v_sn + 8 * ch;
-    }
-    __builtin_amdgcn_global_load_lds(ks, (lds_void*)(Kd + (16 * c.w + 8 * i) * kRowBytes), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds(vs, (lds_void*)(Vd + (16 * c.w + 8 * i) * kRowBytes), 16, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(Kd + (16 * c.w + 8 * i) * kRowBytes),
+                                             16, c.kvo[i], 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)(Vd + (16 * c.w + 8 * i) * kRowBytes),
+                                             16, c.vvo[i], 0, 0, 0);
   }
+}
+
+// v_max3_f32 on raw registers.  fmaxf would first canonicalise every MFMA
+// result (v_max_f32 x, x per operand: IEEE mode quiets signalling NaNs); the
+// scores here are finite or -inf, so the plain three-input max is exact.
+__device__ __forceinline__ float max3_raw(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
+// Max of a lane's 16 scores: a depth-3 tree of seven max3.
+__device__ __forceinline__ float max16(const f32x4 (&sc)[4]) {
+  const float a = max3_raw(sc[0][0], sc[0][1], sc[0][2]);
+  const float b = max3_raw(sc[0][3], sc[1][0], sc[1][1]);
+  const float d = max3_raw(sc[1][2], sc[1][3], sc[2][0]);
+  const float e = max3_raw(sc[2][1], sc[2][2], sc[2][3]);
+  const float f = max3_raw(sc[3][0], sc[3][1], sc[3][2]);
+  return max3_raw(max3_raw(a, b, d), max3_raw(e, f, sc[3][3]), kNegInf);
 }
 
 // One tile: wait for its loads, refill the stage of tile kt-1 with tile kt+2,
@@ -442,10 +471,7 @@ __device__ __forceinline__ void lds_step(LdsCtx& c, int kt, const unsigned char*
         if (!(key <= c.qrow && key < c.S)) sc[blk][i] = kNegInf;
       }
   }
-  float mx = fmaxf(fmaxf(sc[0][0], sc[0][1]), fmaxf(sc[0][2], sc[0][3]));
-#pragma unroll
-  for (int blk = 1; blk < 4; ++blk)
-    mx = fmaxf(mx, fmaxf(fmaxf(sc[blk][0], sc[blk][1]), fmaxf(sc[blk][2], sc[blk][3])));
+  float mx = max16(sc);
   mx *= c.ks2;
   if (__any(mx > c.m_use + kRescaleSlack)) {
     const float m_new = fmaxf(c.m_use, col_max(mx));
@@ -489,8 +515,18 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_lds_kernel(Args a) {
   __shared__ __attribute__((aligned(16))) unsigned char k1[kBN * kRowBytes], v1[kBN * kRowBytes];
   __shared__ __attribute__((aligned(16))) unsigned char k2[kBN * kRowBytes], v2[kBN * kRowBytes];
 
-  const int n_mtiles = gridDim.x;
-  const int mt = n_mtiles - 1 - blockIdx.x;  // heaviest tiles first
+  // Work item -> (query tile, key-tile range), heaviest first: the n_split
+  // split query tiles come as pairs (part 0: keys [0, split_from), part 1:
+  // the rest, diagonal included), then the unsplit tiles in falling order.
+  const int n_mtiles = (a.S + kBM - 1) / kBM;
+  const int x = blockIdx.x;
+  int mt, part = -1;
+  if (x < 2 * a.n_split) {
+    mt = n_mtiles - 1 - (x >> 1);
+    part = x & 1;
+  } else {
+    mt = n_mtiles - 1 - a.n_split - (x - 2 * a.n_split);
+  }
   const int bq = blockIdx.y;
   const int b = bq / a.QH, hq = bq % a.QH;
   const int hk = hq / a.G;
@@ -509,7 +545,10 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_lds_kernel(Args a) {
   c.grp = grp;
   c.w = w;
   const int key_end = (mt + 1) * kBM < S ? (mt + 1) * kBM : S;
-  c.n_ktiles = (key_end + kBN - 1) / kBN;
+  c.n_ktiles = (key_end + kBN - 1) / kBN;  // end of this item's key tiles
+  int kt0 = 0;
+  if (part == 0) c.n_ktiles = a.split_from;
+  if (part == 1) kt0 = a.split_from;
   c.qrow = mt * kBM + w * 16 + col;
   // Loader mapping: lane -> row 8i + lane/8 of the wave's 16, physical chunk lane % 8.
   c.lrow0 = 16 * w + (lane >> 3);
@@ -518,8 +557,8 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_lds_kernel(Args a) {
   for (int i = 0; i < 2; ++i) {
     const int r = c.lrow0 + 8 * i;
     const int ch = c.pch ^ swz(r);
-    c.kp[i] = c.kb + (int64_t)r * c.k_sn + 8 * ch;
-    c.vp[i] = c.vb + (int64_t)r * c.v_sn + 8 * ch;
+    c.kvo[i] = (int)(r * c.k_sn * 2) + 16 * ch;
+    c.vvo[i] = (int)(r * c.v_sn * 2) + 16 * ch;
   }
 
   // ---- Q^T operand (16 rows per wave), rotated in registers; loads go first.
@@ -537,8 +576,8 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_lds_kernel(Args a) {
       qcs[3] = load16(a.sin + co + 32);
     }
   }
-  lds_issue(c, 0, k0, v0);
-  if (c.n_ktiles > 1) lds_issue(c, 1, k1, v1);
+  lds_issue(c, kt0, k0, v0);
+  if (kt0 + 1 < c.n_ktiles) lds_issue(c, kt0 + 1, k1, v1);
   if (kRopeQ) rope_pair(c.qf[0], c.qf[1], qcs[0], qcs[1], qcs[2], qcs[3]);
 
 #pragma unroll
@@ -565,13 +604,27 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_lds_kernel(Args a) {
 #pragma unroll
   for (int t = 0; t < 4; ++t) c.o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int kt = 0; kt < c.n_ktiles; kt += kStages) {
+  for (int kt = kt0; kt < c.n_ktiles; kt += kStages) {
     lds_step(c, kt, k0, v0, k2, v2);
     if (kt + 1 < c.n_ktiles) lds_step(c, kt + 1, k1, v1, k0, v0);
     if (kt + 2 < c.n_ktiles) lds_step(c, kt + 2, k2, v2, k1, v1);
   }
 
   const float l_run = c.l4[0];
+  if (part >= 0) {
+    // Partial of a split query tile: unnormalised o, running max (log2
+    // units) and sum, for the merge kernel.  Layout [bq][split tile][part]
+    // [row][kPartVals]; grp 0 also writes m and l.
+    const int si = n_mtiles - 1 - mt;
+    float* pp = a.part + ((((int64_t)bq * a.n_split + si) * 2 + part) * kBM + w * 16 + col) * kPartVals;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) *reinterpret_cast<f32x4*>(pp + 16 * t + 4 * grp) = c.o[t];
+    if (grp == 0) {
+      pp[64] = c.m_use;
+      pp[65] = l_run;
+    }
+    return;
+  }
   if (c.qrow < S) {
     const float inv = 1.f / l_run;
     f16* op = a.out + b * a.o_sb + hq * a.o_sh + (int64_t)c.qrow * a.o_sn;
@@ -582,6 +635,36 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_lds_kernel(Args a) {
       for (int i = 0; i < 4; ++i) r[i] = (f16)(c.o[t][i] * inv);
       *reinterpret_cast<f16x4*>(op + 16 * t + 4 * grp) = r;
     }
+  }
+}
+
+// Merge of the two partials of each split query tile: grid (n_split, B*QH),
+// thread -> (row, 4 dims).  o = (o0 s0 + o1 s1) / (l0 s0 + l1 s1) with
+// s_i = 2^(m_i - max(m0, m1)), rounded once to fp16.
+__global__ __launch_bounds__(256) void prefill_merge_kernel(Args a) {
+  const int n_mtiles = (a.S + kBM - 1) / kBM;
+  const int si = blockIdx.x, bq = blockIdx.y;
+  const int mt = n_mtiles - 1 - si;
+  const int b = bq / a.QH, hq = bq % a.QH;
+  const float* p0 = a.part + (((int64_t)bq * a.n_split + si) * 2) * kBM * kPartVals;
+  const float* p1 = p0 + kBM * kPartVals;
+  for (int it = threadIdx.x; it < kBM * 16; it += 256) {
+    const int row = it >> 4, d4 = it & 15;
+    const int qrow = mt * kBM + row;
+    const f32x4 o0 = *reinterpret_cast<const f32x4*>(p0 + row * kPartVals + 4 * d4);
+    const f32x4 o1 = *reinterpret_cast<const f32x4*>(p1 + row * kPartVals + 4 * d4);
+    const float m0 = p0[row * kPartVals + 64], l0 = p0[row * kPartVals + 65];
+    const float m1 = p1[row * kPartVals + 64], l1 = p1[row * kPartVals + 65];
+    if (qrow >= a.S) continue;
+    const float m = fmaxf(m0, m1);
+    const float s0 = (m0 == kNegInf) ? 0.f : fast_exp2(m0 - m);
+    const float s1 = (m1 == kNegInf) ? 0.f : fast_exp2(m1 - m);
+    const float inv = 1.f / (l0 * s0 + l1 * s1);
+    const f32x4 o = o0 * s0 + o1 * s1;
+    f16x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = (f16)(o[i] * inv);
+    *reinterpret_cast<f16x4*>(a.out + b * a.o_sb + hq * a.o_sh + (int64_t)qrow * a.o_sn + 4 * d4) = r;
   }
 }
 
@@ -620,6 +703,26 @@ using namespace qf;
 
 static bool aligned16p(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Query tiles below this count are not split (the chain is already short).
+static constexpr int kSplitMinTiles = 8;
+
+static void split_plan(int S, int& split_from, int& n_split) {
+  const int n_mtiles = (S + qf::prefill::kBM - 1) / qf::prefill::kBM;
+  split_from = 0;
+  n_split = 0;
+  if (n_mtiles < kSplitMinTiles) return;
+  split_from = (n_mtiles + 1) / 2;
+  n_split = n_mtiles - split_from;
+}
+
+extern "C" int64_t qf_prefill_workspace_bytes(int B, int QH, int S) {
+  using namespace qf::prefill;
+  if (B < 1 || QH < 1 || S < 1) return 0;
+  int split_from, n_split;
+  split_plan(S, split_from, n_split);
+  return (int64_t)B * QH * n_split * 2 * kBM * kPartVals * (int64_t)sizeof(float);
+}
+
 extern "C" int qf_prefill_attn(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sn,
                                const void* k, int64_t k_sb, int64_t k_sh, int64_t k_sn,
                                const void* v, int64_t v_sb, int64_t v_sh, int64_t v_sn,
@@ -630,6 +733,22 @@ extern "C" int qf_prefill_attn(const void* q, int64_t q_sb, int64_t q_sh, int64_
                                void* out, int64_t o_sb, int64_t o_sh, int64_t o_sn,
                                int B, int QH, int KVH, int S, int D, float scale,
                                void* stream) {
+  return qf_prefill_attn_ws(q, q_sb, q_sh, q_sn, k, k_sb, k_sh, k_sn, v, v_sb, v_sh, v_sn, cos,
+                            sin, cs_sb, cs_sn, k_cache, kc_sb, kc_sh, kc_sn, v_cache, vc_sb, vc_sh,
+                            vc_sn, start_pos, cap, out, o_sb, o_sh, o_sn, B, QH, KVH, S, D, scale,
+                            nullptr, 0, stream);
+}
+
+extern "C" int qf_prefill_attn_ws(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sn,
+                                  const void* k, int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                                  const void* v, int64_t v_sb, int64_t v_sh, int64_t v_sn,
+                                  const void* cos, const void* sin, int64_t cs_sb, int64_t cs_sn,
+                                  void* k_cache, int64_t kc_sb, int64_t kc_sh, int64_t kc_sn,
+                                  void* v_cache, int64_t vc_sb, int64_t vc_sh, int64_t vc_sn,
+                                  int64_t start_pos, int cap,
+                                  void* out, int64_t o_sb, int64_t o_sh, int64_t o_sn,
+                                  int B, int QH, int KVH, int S, int D, float scale,
+                                  void* workspace, int64_t workspace_bytes, void* stream) {
   using namespace qf::prefill;
   if (D != kD) return QF_ERR_UNSUPPORTED;
   if (!q || !k || !v || !out) return QF_ERR_INVALID_ARG;
@@ -667,6 +786,15 @@ extern "C" int qf_prefill_attn(const void* q, int64_t q_sb, int64_t q_sh, int64_
   a.o_sb = o_sb; a.o_sh = o_sh; a.o_sn = o_sn;
   a.B = B; a.QH = QH; a.KVH = KVH; a.G = QH / KVH; a.S = S;
   a.scale_log2 = scale * kLog2e;
+  a.part = nullptr;
+  a.split_from = 0;
+  a.n_split = 0;
+  if (workspace != nullptr && workspace_bytes > 0) {
+    if (!aligned16p(workspace) || workspace_bytes < qf_prefill_workspace_bytes(B, QH, S))
+      return QF_ERR_INVALID_ARG;
+    a.part = static_cast<float*>(workspace);
+    split_plan(S, a.split_from, a.n_split);
+  }
 
   hipStream_t st = static_cast<hipStream_t>(stream);
   dim3 grid((S + kBM - 1) / kBM, B * QH), block(kWaves * 64);
@@ -686,7 +814,14 @@ extern "C" int qf_prefill_attn(const void* q, int64_t q_sb, int64_t q_sh, int64_
     a.v = a.vc + start_pos * a.vc_sn;
     a.v_sb = vc_sb; a.v_sh = vc_sh; a.v_sn = vc_sn;
   }
-  if (rope) hipLaunchKernelGGL((prefill_lds_kernel<true>), grid, block, 0, st, a);
-  else hipLaunchKernelGGL((prefill_lds_kernel<false>), grid, block, 0, st, a);
+  // The streaming kernel addresses a tile's rows with 32-bit byte offsets
+  // and bounds them by the record count of a buffer resource.
+  if (a.k_sn < kD || a.v_sn < kD || a.k_sn * 2 * kBN > 0x7fffffff || a.v_sn * 2 * kBN > 0x7fffffff)
+    return QF_ERR_UNSUPPORTED;
+  const dim3 lgrid(grid.x + a.n_split, B * QH);
+  if (rope) hipLaunchKernelGGL((prefill_lds_kernel<true>), lgrid, block, 0, st, a);
+  else hipLaunchKernelGGL((prefill_lds_kernel<false>), lgrid, block, 0, st, a);
+  if (a.n_split > 0)
+    hipLaunchKernelGGL(prefill_merge_kernel, dim3(a.n_split, B * QH), dim3(256), 0, st, a);
   return (int)hipGetLastError();
 }

@@ -20,7 +20,7 @@ def _declared():
     names = set()
     for header in HEADERS:
         text = header.read_text()
-        names.update(re.findall(r"^\s*(?:const\s+char\*|int)\s+(qf_\w+)\s*\(", text, re.M))
+        names.update(re.findall(r"^\s*(?:const\s+char\*|int|int64_t)\s+(qf_\w+)\s*\(", text, re.M))
     return sorted(names)
 
 
@@ -41,7 +41,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_version_and_error_strings():
     lib = _lib.load()
-    assert lib.qf_abi_version() == 100
+    assert lib.qf_abi_version() == 101
     assert lib.qf_error_string(0) == b"success"
     assert b"invalid" in lib.qf_error_string(-1)
     assert b"unsupported" in lib.qf_error_string(-2)
@@ -129,3 +129,16 @@ def test_step_kernels_reject_bad_arguments():
                                     None, 0, 0, 0, 16, 0, 0, 0, 16, 16, 0, 0,
                                     1, 896, 14, 2, 64, 64, None)
     assert rc == -1  # no key cache
+
+
+def test_prefill_workspace_plan():
+    lib = _lib.load()
+    # Short prompts are not split; S=2048 (32 query tiles) splits the top 16.
+    assert lib.qf_prefill_workspace_bytes(1, 14, 256) == 0
+    assert lib.qf_prefill_workspace_bytes(1, 14, 2048) == 14 * 16 * 2 * 64 * 66 * 4
+    assert lib.qf_prefill_workspace_bytes(2, 14, 2048) == 2 * 14 * 16 * 2 * 64 * 66 * 4
+    # A workspace smaller than the plan is rejected before any launch.
+    rc = lib.qf_prefill_attn_ws(16, 0, 0, 0, 16, 0, 0, 0, 16, 0, 0, 0, None, None, 0, 0,
+                                None, 0, 0, 0, None, 0, 0, 0, 0, 0, 16, 0, 0, 0,
+                                1, 14, 2, 2048, 64, 0.125, 16, 1024, None)
+    assert rc == -1

@@ -91,3 +91,31 @@ def test_first_row_is_first_value(dev):
     out = ops.gqa_flash_prefill(c.query, c.key, c.value).cpu()
     expect = case.value.repeat_interleave(7, dim=1)[:, :, 0]
     assert _err(out[:, :, 0], expect) == 0.0
+
+
+@pytest.mark.parametrize("seq", [512, 1000, 2048])
+def test_split_query_tiles_match_unsplit(dev, seq):
+    """The workspace path (heaviest query tiles split over two workgroups and
+    merged) and the plain entry point both match the oracle."""
+    from qwenforge_amd import _lib
+
+    case = workloads.prefill_case(seq, batch=1, seed=seq)
+    c = case.to(dev)
+    lib = _lib.load()
+    assert lib.qf_prefill_workspace_bytes(1, 14, seq) > 0
+    split = torch.ops.student_qwen.gqa_flash_prefill(c.query, c.key, c.value)
+    plain = torch.empty_like(c.query)
+    rc = lib.qf_prefill_attn(
+        c.query.data_ptr(), *c.query.stride()[:3], c.key.data_ptr(), *c.key.stride()[:3],
+        c.value.data_ptr(), *c.value.stride()[:3], None, None, 0, 0,
+        None, 0, 0, 0, None, 0, 0, 0, 0, 0,
+        plain.data_ptr(), *plain.stride()[:3], 1, 14, 2, seq, 64, 0.125,
+        torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "qf_prefill_attn")
+    torch.cuda.synchronize()
+    ref = oracle.causal_prefill(case.query, case.key, case.value)
+    print(f"[prefill split S={seq}] split err {_err(split.cpu(), ref):.2e} "
+          f"plain err {_err(plain.cpu(), ref):.2e}", flush=True)
+    assert _err(split.cpu(), ref) <= TOL
+    assert _err(plain.cpu(), ref) <= TOL
+    assert _err(split, plain) <= TOL
