@@ -638,9 +638,24 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_lds_kernel(Args a) {
   }
 }
 
-// Merge of the two partials of each split query tile: grid (n_split, B*QH),
-// thread -> (row, 4 dims).  o = (o0 s0 + o1 s1) / (l0 s0 + l1 s1) with
+// One merged (row, 4 dims) item: o = (o0 s0 + o1 s1) / (l0 s0 + l1 s1) with
 // s_i = 2^(m_i - max(m0, m1)), rounded once to fp16.
+__device__ __forceinline__ void merge_write(const Args& a, int b, int hq, int qrow, int d4,
+                                            f32x4 o0, float m0, float l0, f32x4 o1, float m1,
+                                            float l1) {
+  const float m = fmaxf(m0, m1);
+  const float s0 = (m0 == kNegInf) ? 0.f : fast_exp2(m0 - m);
+  const float s1 = (m1 == kNegInf) ? 0.f : fast_exp2(m1 - m);
+  const float inv = 1.f / (l0 * s0 + l1 * s1);
+  const f32x4 o = o0 * s0 + o1 * s1;
+  f16x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = (f16)(o[i] * inv);
+  *reinterpret_cast<f16x4*>(a.out + b * a.o_sb + hq * a.o_sh + (int64_t)qrow * a.o_sn + 4 * d4) = r;
+}
+
+// Merge of the two partials of each split query tile: grid (n_split, B*QH),
+// four (row, 4 dims) items per thread, every load issued before any use.
 __global__ __launch_bounds__(256) void prefill_merge_kernel(Args a) {
   const int n_mtiles = (a.S + kBM - 1) / kBM;
   const int si = blockIdx.x, bq = blockIdx.y;
@@ -648,23 +663,25 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(Args a) {
   const int b = bq / a.QH, hq = bq % a.QH;
   const float* p0 = a.part + (((int64_t)bq * a.n_split + si) * 2) * kBM * kPartVals;
   const float* p1 = p0 + kBM * kPartVals;
-  for (int it = threadIdx.x; it < kBM * 16; it += 256) {
-    const int row = it >> 4, d4 = it & 15;
-    const int qrow = mt * kBM + row;
-    const f32x4 o0 = *reinterpret_cast<const f32x4*>(p0 + row * kPartVals + 4 * d4);
-    const f32x4 o1 = *reinterpret_cast<const f32x4*>(p1 + row * kPartVals + 4 * d4);
-    const float m0 = p0[row * kPartVals + 64], l0 = p0[row * kPartVals + 65];
-    const float m1 = p1[row * kPartVals + 64], l1 = p1[row * kPartVals + 65];
-    if (qrow >= a.S) continue;
-    const float m = fmaxf(m0, m1);
-    const float s0 = (m0 == kNegInf) ? 0.f : fast_exp2(m0 - m);
-    const float s1 = (m1 == kNegInf) ? 0.f : fast_exp2(m1 - m);
-    const float inv = 1.f / (l0 * s0 + l1 * s1);
-    const f32x4 o = o0 * s0 + o1 * s1;
-    f16x4 r;
+  constexpr int kItems = kBM * 16 / 256;
+  f32x4 o0[kItems], o1[kItems];
+  float m0[kItems], l0[kItems], m1[kItems], l1[kItems];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = (f16)(o[i] * inv);
-    *reinterpret_cast<f16x4*>(a.out + b * a.o_sb + hq * a.o_sh + (int64_t)qrow * a.o_sn + 4 * d4) = r;
+  for (int i = 0; i < kItems; ++i) {
+    const int it = threadIdx.x + 256 * i;
+    const int row = it >> 4, d4 = it & 15;
+    o0[i] = *reinterpret_cast<const f32x4*>(p0 + row * kPartVals + 4 * d4);
+    o1[i] = *reinterpret_cast<const f32x4*>(p1 + row * kPartVals + 4 * d4);
+    m0[i] = p0[row * kPartVals + 64];
+    l0[i] = p0[row * kPartVals + 65];
+    m1[i] = p1[row * kPartVals + 64];
+    l1[i] = p1[row * kPartVals + 65];
+  }
+#pragma unroll
+  for (int i = 0; i < kItems; ++i) {
+    const int it = threadIdx.x + 256 * i;
+    const int qrow = mt * kBM + (it >> 4);
+    if (qrow < a.S) merge_write(a, b, hq, qrow, it & 15, o0[i], m0[i], l0[i], o1[i], m1[i], l1[i]);
   }
 }
 
