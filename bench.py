@@ -41,6 +41,8 @@ def _args():
     p.add_argument("--no-extras", action="store_true", help="headline line only")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--prefill-only", action="store_true",
+                   help="time only the config-4 prefill leg (for kernel profiles)")
     p.add_argument("--pmc-sample", action="store_true",
                    help="run a short fixed kernel sequence for rocprofv3 --pmc and exit")
     return p.parse_args()
@@ -324,6 +326,13 @@ def main():
     if args.pmc_sample:
         pmc_sample(dev)
         return
+    if args.prefill_only:
+        pf = bench_prefill(args.steps, args.warmup, dev)
+        tf = pf["flops"] / (pf["us_per_layer"] * 1e-6) / 1e12
+        print(json.dumps({"prefill_cfg4": {"us_per_layer": round(pf["us_per_layer"], 3),
+                                           "TFLOPs": round(tf, 2),
+                                           "mfma_frac": round(tf / FP16_MFMA_PEAK_TFLOPS, 4)}}))
+        return
 
     r = bench_ragged_decode(args.steps, args.warmup, dev)
     ms = r["ms_per_step"]
@@ -362,7 +371,7 @@ def main():
             "unit": "GB/s",
             "frac": round(split_gbs / HBM_PEAK_GBS, 4),
             "traffic": _traffic(),
-            "kernel": "qf::decode_split_kernel<8, true, 1> (qf_decode_split, partial mode)",
+            "kernel": "qf::decode_split_kernel<8, 1, 1> (qf_decode_split: 8 waves, vector bias, partial mode)",
             "bytes_per_launch": int(launch_bytes),
             "avg_launch_us": round(us_split, 3),
             "combine_kernel_avg_us": (None if r["ms_combine"] is None

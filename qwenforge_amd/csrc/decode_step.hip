@@ -649,18 +649,28 @@ __global__ __launch_bounds__(256) void argmax_step_kernel(FinArgs a) {
   const int64_t s = a.step != nullptr ? a.step[0] : 0;
   const int64_t p = (a.pos != nullptr && tid < a.B) ? a.pos[tid] : 0;
   const int64_t wi = (a.write_index != nullptr && tid == 0) ? a.write_index[0] : 0;
+  // Four keys per row per thread and round, all rows' loads issued together
+  // (indices past n_blocks re-read the last key).
   uint64_t k[kMaxB];
 #pragma unroll
-  for (int b = 0; b < kMaxB; ++b) {
-    k[b] = 0;
-    if (b < a.B) {
-      for (int j = tid; j < a.n_blocks; j += 256) {
-        const uint64_t v = a.keys[(int64_t)b * a.n_blocks + j];
-        k[b] = v > k[b] ? v : k[b];
+  for (int b = 0; b < kMaxB; ++b) k[b] = 0;
+  const int rows = a.B;
+  for (int j0 = tid; j0 < a.n_blocks; j0 += 4 * 256) {
+    uint64_t v[kMaxB][4];
+#pragma unroll
+    for (int b = 0; b < kMaxB; ++b)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int j = min(j0 + 256 * u, a.n_blocks - 1);
+        v[b][u] = a.keys[(int64_t)min(b, rows - 1) * a.n_blocks + j];
       }
-    }
-    part[b][tid] = k[b];
+#pragma unroll
+    for (int b = 0; b < kMaxB; ++b)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) k[b] = v[b][u] > k[b] ? v[b][u] : k[b];
   }
+#pragma unroll
+  for (int b = 0; b < kMaxB; ++b) part[b][tid] = k[b];
   __syncthreads();
   for (int o = 128; o > 0; o >>= 1) {
     if (tid < o) {
