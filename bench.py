@@ -198,6 +198,26 @@ def bench_bandwidth_decode(steps, warmup, dev, batch, length):
                 us_full=ms_full * 1e3, us_split=ms_split * 1e3, bytes=nbytes)
 
 
+def hbm_copy_ceiling(dev, mib=512, reps=20):
+    """Practical HBM rate on this box: a plain device copy of `mib` MiB
+    (torch.Tensor.copy_), counted as read + write bytes per second."""
+    import torch
+
+    src = torch.empty(mib << 19, device=dev, dtype=torch.float16)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
+    return 2 * src.numel() * 2 / (ms * 1e-3) / 1e9
+
+
 def bench_prefill(steps, warmup, dev):
     """Config 4: causal prefill S=2048 with fused RoPE + cache append."""
     import torch
@@ -402,6 +422,10 @@ def main():
                 "merge": "fused single launch" if x["fused"] else "split + combine launches",
             }
         line["bandwidth_decode"] = bw
+        copy_gbs = hbm_copy_ceiling(dev)
+        line["hbm_copy_ceiling"] = {"GBps": round(copy_gbs, 1),
+                                    "frac_of_peak": round(copy_gbs / HBM_PEAK_GBS, 4),
+                                    "what": "torch copy_ of 512 MiB, read + write bytes / time"}
         pf = bench_prefill(args.steps, args.warmup, dev)
         tf = pf["flops"] / (pf["us_per_layer"] * 1e-6) / 1e12
         line["prefill_cfg4"] = {
