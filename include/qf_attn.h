@@ -171,6 +171,34 @@ int qf_prefill_attn_ws(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sn,
 int64_t qf_prefill_workspace_bytes(int B, int QH, int S);
 
 /*
+ * Ragged (variable-length) causal prefill of B packed rows, with the same
+ * optional RoPE and cache-append fusions.  Replaces _prefill_ragged
+ * (student_engine.py:1162-1204), which runs _prefill once per row and copies
+ * each row's K/V into cache[row, :, :len] -- here one launch covers every row.
+ *
+ *   q (T, QH, D), k/v (T, KVH, D), out (T, QH, D): the B rows packed along
+ *          the token axis (strides *_sh per head, *_sn per token); row b is
+ *          tokens [cu_seqlens[b], cu_seqlens[b+1]) (int32 device array of
+ *          B+1 entries, cu_seqlens[0] = 0, total = T = cu_seqlens[B]).
+ *   max_seqlen  the longest row (sizes the grid; rows are clamped to it and
+ *          to [0, total), so no cu content reads or writes out of bounds).
+ *   cos, sin (T, D): per-token tables (each row's positions 0..len-1),
+ *          token stride cs_sn.  RoPE requires the cache (both or neither).
+ *   k_cache, v_cache (B, KVH, cap, D): token i of row b goes to slot
+ *          start_pos + i of row b.  Requires start_pos + max_seqlen <= cap.
+ */
+int qf_prefill_varlen(const void* q, int64_t q_sh, int64_t q_sn,
+                      const void* k, int64_t k_sh, int64_t k_sn,
+                      const void* v, int64_t v_sh, int64_t v_sn,
+                      const int32_t* cu_seqlens, int total, int max_seqlen,
+                      const void* cos, const void* sin, int64_t cs_sn,
+                      void* k_cache, int64_t kc_sb, int64_t kc_sh, int64_t kc_sn,
+                      void* v_cache, int64_t vc_sb, int64_t vc_sh, int64_t vc_sn,
+                      int64_t start_pos, int cap,
+                      void* out, int64_t o_sh, int64_t o_sn,
+                      int B, int QH, int KVH, int D, float scale, void* stream);
+
+/*
  * One-token RoPE + KV-cache append (decode).
  *
  * Replaces the eager RoPE of the graph step (student_engine.py:927-928, with

@@ -70,6 +70,19 @@ SIGNATURES = {
         _vp, _i64, _vp,                 # workspace, workspace_bytes, stream
     ],
     "qf_prefill_workspace_bytes": [_i32, _i32, _i32],
+    "qf_prefill_varlen": [
+        _vp, _i64, _i64,                # q, q_sh, q_sn
+        _vp, _i64, _i64,                # k
+        _vp, _i64, _i64,                # v
+        _vp, _i32, _i32,                # cu_seqlens, total, max_seqlen
+        _vp, _vp, _i64,                 # cos, sin, cs_sn
+        _vp, _i64, _i64, _i64,          # k_cache
+        _vp, _i64, _i64, _i64,          # v_cache
+        _i64, _i32,                     # start_pos, cap
+        _vp, _i64, _i64,                # out, o_sh, o_sn
+        _i32, _i32, _i32, _i32,         # B, QH, KVH, D
+        _f32, _vp,                      # scale, stream
+    ],
     "qf_rope_append": [
         _vp, _i64, _i64,                # q, q_sb, q_sh
         _vp, _i64, _i64,                # k

@@ -66,7 +66,28 @@ struct Args {
   // kernel.  n_split = number of split query tiles (0: no split).
   float* part;
   int split_from, n_split;
+  // Packed variable-length rows (ragged prefill): row b's tokens are
+  // [cu[b], cu[b+1]) of q/k/v/out/cos/sin, whose batch strides are then 0;
+  // S holds the longest row.  kv_packed: k/v are those packed inputs (1) or
+  // the per-row cache (0).  cu == nullptr: every row has S tokens.
+  const int* cu;
+  int total;  // packed token count (bounds every row)
+  int kv_packed;
 };
+
+// Token count and first packed token of row b, clamped to [0, total) and to
+// the longest row S, so any cu contents keep every access in bounds.
+__device__ __forceinline__ void row_span(const Args& a, int b, int& S, int64_t& tok0) {
+  if (a.cu != nullptr) {
+    const int lo = min(max(a.cu[b], 0), a.total);
+    const int hi = min(max(a.cu[b + 1], lo), a.total);
+    tok0 = lo;
+    S = min(hi - lo, a.S);
+  } else {
+    tok0 = 0;
+    S = a.S;
+  }
+}
 
 // Registers holding one K/V tile between its global load and its LDS store.
 // The K rotation happens at store time, so the loads stay in flight while the
@@ -533,11 +554,15 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_lds_kernel(Args a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   const int col = lane & 15, grp = lane >> 4;
-  const int S = a.S;
+  int S;
+  int64_t tok0;
+  row_span(a, b, S, tok0);
+  if (mt * kBM >= S) return;  // a shorter packed row: this query tile is empty
 
   LdsCtx c;
-  c.kb = a.k + b * a.k_sb + hk * a.k_sh;
-  c.vb = a.v + b * a.v_sb + hk * a.v_sh;
+  const int64_t kvt = a.kv_packed ? tok0 : 0;
+  c.kb = a.k + b * a.k_sb + kvt * a.k_sn + hk * a.k_sh;
+  c.vb = a.v + b * a.v_sb + kvt * a.v_sn + hk * a.v_sh;
   c.k_sn = a.k_sn;
   c.v_sn = a.v_sn;
   c.S = S;
@@ -565,11 +590,11 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_lds_kernel(Args a) {
   f16x8 qcs[4];
   {
     const int qr = c.qrow < S ? c.qrow : S - 1;
-    const f16* qp = a.q + b * a.q_sb + hq * a.q_sh + (int64_t)qr * a.q_sn + 8 * grp;
+    const f16* qp = a.q + b * a.q_sb + hq * a.q_sh + (tok0 + qr) * a.q_sn + 8 * grp;
     c.qf[0] = load16(qp);
     c.qf[1] = load16(qp + 32);
     if (kRopeQ) {
-      const int64_t co = b * a.cs_sb + (int64_t)qr * a.cs_sn + 8 * grp;
+      const int64_t co = b * a.cs_sb + (tok0 + qr) * a.cs_sn + 8 * grp;
       qcs[0] = load16(a.cos + co);
       qcs[1] = load16(a.sin + co);
       qcs[2] = load16(a.cos + co + 32);
@@ -627,7 +652,7 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_lds_kernel(Args a) {
   }
   if (c.qrow < S) {
     const float inv = 1.f / l_run;
-    f16* op = a.out + b * a.o_sb + hq * a.o_sh + (int64_t)c.qrow * a.o_sn;
+    f16* op = a.out + b * a.o_sb + hq * a.o_sh + (tok0 + c.qrow) * a.o_sn;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       f16x4 r;
@@ -693,13 +718,17 @@ __global__ __launch_bounds__(256) void rope_kv_prefill_kernel(Args a) {
   const int sub = threadIdx.x & 15;
   const int bh = blockIdx.y;
   const int b = bh / a.KVH, h = bh % a.KVH;
-  if (tok >= a.S || sub >= 12) return;
+  int S;
+  int64_t tok0;
+  row_span(a, b, S, tok0);
+  if (tok >= S || sub >= 12) return;
   const int64_t slot = a.start_pos + tok;
+  const int64_t t = tok0 + tok;  // packed token index (== tok for equal-length rows)
   if (sub < 4) {
-    const f16* src = a.k + b * a.k_sb + h * a.k_sh + (int64_t)tok * a.k_sn + 8 * sub;
+    const f16* src = a.k + b * a.k_sb + h * a.k_sh + t * a.k_sn + 8 * sub;
     f16x8 lo = load16(src), hi = load16(src + 32);
     if (a.cos != nullptr) {
-      const int64_t co = b * a.cs_sb + (int64_t)tok * a.cs_sn + 8 * sub;
+      const int64_t co = b * a.cs_sb + t * a.cs_sn + 8 * sub;
       rope_pair(lo, hi, load16(a.cos + co), load16(a.sin + co), load16(a.cos + co + 32),
                 load16(a.sin + co + 32));
     }
@@ -709,7 +738,7 @@ __global__ __launch_bounds__(256) void rope_kv_prefill_kernel(Args a) {
   } else {
     const int c = sub - 4;
     store16(a.vc + b * a.vc_sb + h * a.vc_sh + slot * a.vc_sn + 8 * c,
-            load16(a.v + b * a.v_sb + h * a.v_sh + (int64_t)tok * a.v_sn + 8 * c));
+            load16(a.v + b * a.v_sb + h * a.v_sh + t * a.v_sn + 8 * c));
   }
 }
 
@@ -756,6 +785,88 @@ extern "C" int qf_prefill_attn(const void* q, int64_t q_sb, int64_t q_sh, int64_
                             nullptr, 0, stream);
 }
 
+using qf::prefill::Args;
+
+// Shared launch sequence of the dense and the packed (varlen) entry points;
+// `a` is filled and validated.  Returns 0 or a QF_ERR_* / hipError_t code.
+static int prefill_launch(Args a, bool rope, bool append, hipStream_t st) {
+  using namespace qf::prefill;
+  const int B = a.B, QH = a.QH, KVH = a.KVH, S = a.S;
+  // The streaming kernel addresses a tile's rows with 32-bit byte offsets and
+  // bounds them by the record count of a buffer resource; check its source
+  // (the cache when appending) before anything is launched.
+  const int64_t ksn = append ? a.kc_sn : a.k_sn, vsn = append ? a.vc_sn : a.v_sn;
+  if (!(rope && !append) &&
+      (ksn < kD || vsn < kD || ksn * 2 * kBN > 0x7fffffff || vsn * 2 * kBN > 0x7fffffff))
+    return QF_ERR_UNSUPPORTED;
+  dim3 grid((S + kBM - 1) / kBM, B * QH), block(kWaves * 64);
+  if (rope && !append) {
+    // No cache to hold the rotated keys: rotate K in registers tile by tile.
+    if (a.cu != nullptr) return QF_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL((prefill_kernel<true, false>), grid, block, 0, st, a);
+    return (int)hipGetLastError();
+  }
+  if (append) {
+    // Pre-pass: rotated K (or K as is) and V into the cache; then stream the
+    // finished rows back from the cache.
+    hipLaunchKernelGGL(rope_kv_prefill_kernel, dim3((S + 15) / 16, B * KVH), dim3(256), 0, st, a);
+    a.k = a.kc + a.start_pos * a.kc_sn;
+    a.k_sb = a.kc_sb; a.k_sh = a.kc_sh; a.k_sn = a.kc_sn;
+    a.v = a.vc + a.start_pos * a.vc_sn;
+    a.v_sb = a.vc_sb; a.v_sh = a.vc_sh; a.v_sn = a.vc_sn;
+    a.kv_packed = 0;
+  }
+  const dim3 lgrid(grid.x + a.n_split, B * QH);
+  if (rope) hipLaunchKernelGGL((prefill_lds_kernel<true>), lgrid, block, 0, st, a);
+  else hipLaunchKernelGGL((prefill_lds_kernel<false>), lgrid, block, 0, st, a);
+  if (a.n_split > 0)
+    hipLaunchKernelGGL(prefill_merge_kernel, dim3(a.n_split, B * QH), dim3(256), 0, st, a);
+  return (int)hipGetLastError();
+}
+
+static int fill_common(Args& a, const void* q, const void* k, const void* v, const void* cos,
+                       const void* sin, void* k_cache, int64_t kc_sb, int64_t kc_sh, int64_t kc_sn,
+                       void* v_cache, int64_t vc_sb, int64_t vc_sh, int64_t vc_sn,
+                       int64_t start_pos, int cap, void* out, int B, int QH, int KVH, int S,
+                       int D, float scale, bool& rope, bool& append) {
+  using namespace qf::prefill;
+  if (D != kD) return QF_ERR_UNSUPPORTED;
+  if (!q || !k || !v || !out) return QF_ERR_INVALID_ARG;
+  if (B < 1 || KVH < 1 || QH < KVH || QH % KVH != 0 || S < 1) return QF_ERR_INVALID_ARG;
+  if ((int64_t)B * QH > 65535) return QF_ERR_INVALID_ARG;
+  rope = cos != nullptr || sin != nullptr;
+  if (rope && (!cos || !sin)) return QF_ERR_INVALID_ARG;
+  append = k_cache != nullptr || v_cache != nullptr;
+  if (append && (!k_cache || !v_cache)) return QF_ERR_INVALID_ARG;
+  if (append && (start_pos < 0 || start_pos + S > cap)) return QF_ERR_INVALID_ARG;
+  if (!aligned16p(q) || !aligned16p(k) || !aligned16p(v)) return QF_ERR_INVALID_ARG;
+  if ((reinterpret_cast<uintptr_t>(out) & 7u)) return QF_ERR_INVALID_ARG;
+  if (rope && (!aligned16p(cos) || !aligned16p(sin))) return QF_ERR_INVALID_ARG;
+  if (append && (!aligned16p(k_cache) || !aligned16p(v_cache) ||
+                 ((kc_sb | kc_sh | kc_sn | vc_sb | vc_sh | vc_sn) & 7)))
+    return QF_ERR_INVALID_ARG;
+  a.q = static_cast<const f16*>(q);
+  a.k = static_cast<const f16*>(k);
+  a.v = static_cast<const f16*>(v);
+  a.cos = static_cast<const f16*>(cos);
+  a.sin = static_cast<const f16*>(sin);
+  a.kc = static_cast<f16*>(k_cache);
+  a.kc_sb = kc_sb; a.kc_sh = kc_sh; a.kc_sn = kc_sn;
+  a.vc = static_cast<f16*>(v_cache);
+  a.vc_sb = vc_sb; a.vc_sh = vc_sh; a.vc_sn = vc_sn;
+  a.start_pos = start_pos;
+  a.out = static_cast<f16*>(out);
+  a.B = B; a.QH = QH; a.KVH = KVH; a.G = QH / KVH; a.S = S;
+  a.scale_log2 = scale * kLog2e;
+  a.part = nullptr;
+  a.split_from = 0;
+  a.n_split = 0;
+  a.cu = nullptr;
+  a.total = 0;
+  a.kv_packed = 1;
+  return QF_OK;
+}
+
 extern "C" int qf_prefill_attn_ws(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sn,
                                   const void* k, int64_t k_sb, int64_t k_sh, int64_t k_sn,
                                   const void* v, int64_t v_sb, int64_t v_sh, int64_t v_sn,
@@ -767,78 +878,57 @@ extern "C" int qf_prefill_attn_ws(const void* q, int64_t q_sb, int64_t q_sh, int
                                   int B, int QH, int KVH, int S, int D, float scale,
                                   void* workspace, int64_t workspace_bytes, void* stream) {
   using namespace qf::prefill;
-  if (D != kD) return QF_ERR_UNSUPPORTED;
-  if (!q || !k || !v || !out) return QF_ERR_INVALID_ARG;
-  if (B < 1 || KVH < 1 || QH < KVH || QH % KVH != 0 || S < 1) return QF_ERR_INVALID_ARG;
-  if ((int64_t)B * QH > 65535) return QF_ERR_INVALID_ARG;
-  const bool rope = cos != nullptr || sin != nullptr;
-  if (rope && (!cos || !sin)) return QF_ERR_INVALID_ARG;
-  const bool append = k_cache != nullptr || v_cache != nullptr;
-  if (append && (!k_cache || !v_cache)) return QF_ERR_INVALID_ARG;
-  if (append && (start_pos < 0 || start_pos + S > cap)) return QF_ERR_INVALID_ARG;
-  if (!aligned16p(q) || !aligned16p(k) || !aligned16p(v)) return QF_ERR_INVALID_ARG;
-  if ((q_sb | q_sh | q_sn | k_sb | k_sh | k_sn | v_sb | v_sh | v_sn) & 7) return QF_ERR_INVALID_ARG;
-  if ((reinterpret_cast<uintptr_t>(out) & 7u) || ((o_sb | o_sh | o_sn) & 3)) return QF_ERR_INVALID_ARG;
-  if (rope && (!aligned16p(cos) || !aligned16p(sin) || ((cs_sb | cs_sn) & 7))) return QF_ERR_INVALID_ARG;
-  if (append && (!aligned16p(k_cache) || !aligned16p(v_cache) ||
-                 ((kc_sb | kc_sh | kc_sn | vc_sb | vc_sh | vc_sn) & 7)))
-    return QF_ERR_INVALID_ARG;
-
   Args a;
-  a.q = static_cast<const f16*>(q);
+  bool rope, append;
+  const int rc = fill_common(a, q, k, v, cos, sin, k_cache, kc_sb, kc_sh, kc_sn, v_cache, vc_sb,
+                             vc_sh, vc_sn, start_pos, cap, out, B, QH, KVH, S, D, scale, rope,
+                             append);
+  if (rc != QF_OK) return rc;
+  if ((q_sb | q_sh | q_sn | k_sb | k_sh | k_sn | v_sb | v_sh | v_sn) & 7) return QF_ERR_INVALID_ARG;
+  if ((o_sb | o_sh | o_sn) & 3) return QF_ERR_INVALID_ARG;
+  if (rope && ((cs_sb | cs_sn) & 7)) return QF_ERR_INVALID_ARG;
   a.q_sb = q_sb; a.q_sh = q_sh; a.q_sn = q_sn;
-  a.k = static_cast<const f16*>(k);
   a.k_sb = k_sb; a.k_sh = k_sh; a.k_sn = k_sn;
-  a.v = static_cast<const f16*>(v);
   a.v_sb = v_sb; a.v_sh = v_sh; a.v_sn = v_sn;
-  a.cos = static_cast<const f16*>(cos);
-  a.sin = static_cast<const f16*>(sin);
   a.cs_sb = cs_sb; a.cs_sn = cs_sn;
-  a.kc = static_cast<f16*>(k_cache);
-  a.kc_sb = kc_sb; a.kc_sh = kc_sh; a.kc_sn = kc_sn;
-  a.vc = static_cast<f16*>(v_cache);
-  a.vc_sb = vc_sb; a.vc_sh = vc_sh; a.vc_sn = vc_sn;
-  a.start_pos = start_pos;
-  a.out = static_cast<f16*>(out);
   a.o_sb = o_sb; a.o_sh = o_sh; a.o_sn = o_sn;
-  a.B = B; a.QH = QH; a.KVH = KVH; a.G = QH / KVH; a.S = S;
-  a.scale_log2 = scale * kLog2e;
-  a.part = nullptr;
-  a.split_from = 0;
-  a.n_split = 0;
   if (workspace != nullptr && workspace_bytes > 0) {
     if (!aligned16p(workspace) || workspace_bytes < qf_prefill_workspace_bytes(B, QH, S))
       return QF_ERR_INVALID_ARG;
     a.part = static_cast<float*>(workspace);
     split_plan(S, a.split_from, a.n_split);
   }
+  return prefill_launch(a, rope, append, static_cast<hipStream_t>(stream));
+}
 
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  dim3 grid((S + kBM - 1) / kBM, B * QH), block(kWaves * 64);
-  if (rope && !append) {
-    // No cache to hold the rotated keys: rotate K in registers tile by tile.
-    hipLaunchKernelGGL((prefill_kernel<true, false>), grid, block, 0, st, a);
-    return (int)hipGetLastError();
-  }
-  if (append) {
-    // Pre-pass: rotated K (or K as is) and V into the cache; then stream the
-    // finished rows back from the cache.
-    Args pre = a;
-    hipLaunchKernelGGL(rope_kv_prefill_kernel, dim3((S + 15) / 16, B * KVH), dim3(256), 0, st,
-                       pre);
-    a.k = a.kc + start_pos * a.kc_sn;
-    a.k_sb = kc_sb; a.k_sh = kc_sh; a.k_sn = kc_sn;
-    a.v = a.vc + start_pos * a.vc_sn;
-    a.v_sb = vc_sb; a.v_sh = vc_sh; a.v_sn = vc_sn;
-  }
-  // The streaming kernel addresses a tile's rows with 32-bit byte offsets
-  // and bounds them by the record count of a buffer resource.
-  if (a.k_sn < kD || a.v_sn < kD || a.k_sn * 2 * kBN > 0x7fffffff || a.v_sn * 2 * kBN > 0x7fffffff)
-    return QF_ERR_UNSUPPORTED;
-  const dim3 lgrid(grid.x + a.n_split, B * QH);
-  if (rope) hipLaunchKernelGGL((prefill_lds_kernel<true>), lgrid, block, 0, st, a);
-  else hipLaunchKernelGGL((prefill_lds_kernel<false>), lgrid, block, 0, st, a);
-  if (a.n_split > 0)
-    hipLaunchKernelGGL(prefill_merge_kernel, dim3(a.n_split, B * QH), dim3(256), 0, st, a);
-  return (int)hipGetLastError();
+extern "C" int qf_prefill_varlen(const void* q, int64_t q_sh, int64_t q_sn,
+                                 const void* k, int64_t k_sh, int64_t k_sn,
+                                 const void* v, int64_t v_sh, int64_t v_sn,
+                                 const int32_t* cu_seqlens, int total, int max_seqlen,
+                                 const void* cos, const void* sin, int64_t cs_sn,
+                                 void* k_cache, int64_t kc_sb, int64_t kc_sh, int64_t kc_sn,
+                                 void* v_cache, int64_t vc_sb, int64_t vc_sh, int64_t vc_sn,
+                                 int64_t start_pos, int cap,
+                                 void* out, int64_t o_sh, int64_t o_sn,
+                                 int B, int QH, int KVH, int D, float scale, void* stream) {
+  using namespace qf::prefill;
+  if (!cu_seqlens || total < 1) return QF_ERR_INVALID_ARG;
+  Args a;
+  bool rope, append;
+  const int rc = fill_common(a, q, k, v, cos, sin, k_cache, kc_sb, kc_sh, kc_sn, v_cache, vc_sb,
+                             vc_sh, vc_sn, start_pos, cap, out, B, QH, KVH, max_seqlen, D, scale,
+                             rope, append);
+  if (rc != QF_OK) return rc;
+  if (rope && !append) return QF_ERR_UNSUPPORTED;  // rotated keys need the cache
+  if ((q_sh | q_sn | k_sh | k_sn | v_sh | v_sn) & 7) return QF_ERR_INVALID_ARG;
+  if ((o_sh | o_sn) & 3) return QF_ERR_INVALID_ARG;
+  if (rope && (cs_sn & 7)) return QF_ERR_INVALID_ARG;
+  a.q_sb = 0; a.q_sh = q_sh; a.q_sn = q_sn;
+  a.k_sb = 0; a.k_sh = k_sh; a.k_sn = k_sn;
+  a.v_sb = 0; a.v_sh = v_sh; a.v_sn = v_sn;
+  a.cs_sb = 0; a.cs_sn = cs_sn;
+  a.o_sb = 0; a.o_sh = o_sh; a.o_sn = o_sn;
+  a.cu = cu_seqlens;
+  a.total = total;
+  return prefill_launch(a, rope, append, static_cast<hipStream_t>(stream));
 }

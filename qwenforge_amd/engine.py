@@ -2,6 +2,10 @@
 
 Mirrors the reference's cached generation path without the tokenizer:
 
+* ``prefill_ragged`` / ``generate_ragged`` -- ``_prefill_ragged``
+  (SE:1162-1204) and the padded-batch decode of ``generate`` (SE:1241-1335)
+  for variable-length prompts: rows packed along the token axis, one varlen
+  prefill launch per layer, decode over the bias-masked holes.
 * ``prefill`` -- ``StudentEngine._prefill`` (SE:679-737): per layer RMSNorm,
   fused QKV projection, then ONE fused HIP launch does rotate-half RoPE, the
   causal GQA attention and the KV-cache append (it replaces the eager RoPE
@@ -97,6 +101,42 @@ class DecodeEngine:
             hidden = residual + self._mlp(self._rms(hidden, layer["post_norm"]), layer)
         last = self._rms(hidden[:, -1], self.w["final_norm"])
         return F.linear(last, self.w["lm_head"])
+
+    @torch.no_grad()
+    def prefill_ragged(self, prompts, caches):
+        """Variable-length prompts (a list of 1-D id tensors) -> last-token logits (B, vocab).
+
+        ``_prefill_ragged`` (SE:1162-1204) runs ``_prefill`` once per row; here
+        the rows are packed along the token axis, so every projection is one
+        GEMM over all tokens and one varlen launch does RoPE, the cache append
+        (slots [0, len_b) of row b) and the causal attention of every row.
+        """
+        cfg = self.cfg
+        dev = self.device
+        lengths = [int(p.numel()) for p in prompts]
+        ids = torch.cat([p.reshape(-1).to(dev) for p in prompts])
+        total = ids.numel()
+        starts = [0]
+        for n in lengths:
+            starts.append(starts[-1] + n)
+        cu = torch.tensor(starts, dtype=torch.int32, device=dev)
+        pos = torch.cat([torch.arange(n, device=dev) for n in lengths])
+        cos, sin = cos_sin(pos, self.inv_freq)                 # (T, D): each row's own positions
+        qw, kvw = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+        hidden = F.embedding(ids, self.w["embed"])
+        for layer, (kc, vc) in zip(self.w["layers"], caches):
+            residual = hidden
+            proj = F.linear(self._rms(hidden, layer["input_norm"]), layer["qkv_weight"],
+                            layer["qkv_bias"])
+            q = proj[:, :qw].view(total, cfg.heads, cfg.head_dim)
+            k = proj[:, qw:qw + kvw].view(total, cfg.kv_heads, cfg.head_dim)
+            v = proj[:, qw + kvw:].view(total, cfg.kv_heads, cfg.head_dim)
+            att = ops.prefill_varlen(q, k, v, cu, max(lengths), cos, sin, kc, vc, 0)
+            hidden = residual + F.linear(att.reshape(total, cfg.hidden), layer["o_weight"])
+            residual = hidden
+            hidden = residual + self._mlp(self._rms(hidden, layer["post_norm"]), layer)
+        last = hidden[cu[1:].long() - 1]
+        return F.linear(self._rms(last, self.w["final_norm"]), self.w["lm_head"])
 
     # ------------------------------------------------------------------ decode
     def _step(self, ctx):
@@ -241,6 +281,47 @@ class DecodeEngine:
         torch.cuda.synchronize(self.device)
         ctx["graph"] = graph
         return graph
+
+    @torch.no_grad()
+    def generate_ragged(self, prompts, max_new_tokens: int, timing: dict | None = None):
+        """Greedy ids (B, max_new_tokens) for variable-length prompts (list of 1-D tensors).
+
+        The reference's padded-batch semantics (SE:1241-1335): capacity =
+        roundup64(max_len + new - 1); row b's prompt fills slots [0, len_b);
+        decode step t writes the shared slot max_len + t - 1 at position
+        len_b + t - 1, and the bias masks the holes [len_b, max_len).
+        """
+        b = len(prompts)
+        lengths = [int(p.numel()) for p in prompts]
+        p_max = max(lengths)
+        cap = (p_max + max(max_new_tokens - 1, 0) + 63) // 64 * 64
+        caches = self.new_caches(b, cap)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        ev[0].record()
+        logits = self.prefill_ragged(prompts, caches)
+        first = torch.argmax(logits, dim=-1)
+        ev[1].record()
+        mask = torch.zeros(b, cap, dtype=torch.bool, device=self.device)
+        for i, n in enumerate(lengths):
+            mask[i, :n] = True
+        ctx = self.make_context(caches, b, max_new_tokens, bias_mask=mask)
+        self.capture(ctx)
+        ctx["rows"][:, 0] = first
+        ctx["token"].copy_(first)
+        ctx["pos"].copy_(torch.tensor(lengths, device=self.device))
+        ctx["write"].fill_(p_max)
+        ctx["step"].fill_(1)
+        torch.cuda.synchronize(self.device)
+        ev[2].record()
+        for _ in range(1, max_new_tokens):
+            ctx["graph"].replay()
+        ev[3].record()
+        torch.cuda.synchronize(self.device)
+        if timing is not None:
+            timing["prefill_ms"] = ev[0].elapsed_time(ev[1])
+            timing["decode_ms"] = ev[2].elapsed_time(ev[3])
+        self._ctx = ctx
+        return ctx["rows"].clone()
 
     @torch.no_grad()
     def generate(self, input_ids: torch.Tensor, max_new_tokens: int, timing: dict | None = None):

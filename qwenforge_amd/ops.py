@@ -14,6 +14,9 @@ library or a CPU tensor raises.
   append of SE:715-716 fused in.
 * ``rope_append(q, k, v, cos, sin, key_cache, value_cache, write_index)``
   -- the graph step's RoPE + ``index_copy_`` append (SE:927-932).
+* ``prefill_varlen(q, k, v, cu_seqlens, max_seqlen, cos, sin, key_cache,
+  value_cache)`` -- the ragged prefill of ``_prefill_ragged`` (SE:1162-1204)
+  over packed rows in one launch.
 """
 
 from __future__ import annotations
@@ -357,6 +360,73 @@ def _prefill_launch(query, key, value, out, cos=None, sin=None, key_cache=None,
             b, qh, kvh, s, d, float(d ** -0.5),
             _ptr(ws), ws_bytes, _stream(query.device))
     _lib.check(rc, "qf_prefill_attn_ws")
+    return out
+
+
+def prefill_varlen(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                   cu_seqlens: torch.Tensor, max_seqlen: int, cos: torch.Tensor | None = None,
+                   sin: torch.Tensor | None = None, key_cache: torch.Tensor | None = None,
+                   value_cache: torch.Tensor | None = None, start_pos: int = 0) -> torch.Tensor:
+    """Ragged causal prefill of packed rows (``_prefill_ragged``, SE:1162-1204, in one launch).
+
+    query (T, QH, 64), key/value (T, KVH, 64): rows packed along the token axis;
+    ``cu_seqlens`` (B+1,) int32 on the device: row b is tokens
+    [cu[b], cu[b+1]).  Optional ``cos``/``sin`` (T, 64) per-token tables (each
+    row's own positions) rotate q and k; with ``key_cache``/``value_cache``
+    (B, KVH, cap, 64) token i of row b is written to slot start_pos + i of row
+    b (RoPE needs the caches).  Returns (T, QH, 64).
+    """
+    for n, t in (("query", query), ("key", key), ("value", value)):
+        _require_cuda_fp16(n, t, 3)
+    t_, qh, d = query.shape
+    kvh = key.shape[1]
+    if key.shape != (t_, kvh, d) or value.shape != key.shape or qh % kvh != 0:
+        raise ValueError("packed prefill shapes: query (T, QH, D), key/value (T, KVH, D)")
+    if cu_seqlens.dtype != torch.int32 or cu_seqlens.dim() != 1 or cu_seqlens.device != query.device:
+        raise TypeError("cu_seqlens must be a 1-D int32 device tensor")
+    b = cu_seqlens.numel() - 1
+    if b < 1 or not 1 <= max_seqlen <= t_:
+        raise ValueError(f"need B >= 1 rows and 1 <= max_seqlen <= T (got {b}, {max_seqlen})")
+    cs_sn = 0
+    if (cos is None) != (sin is None):
+        raise ValueError("cos and sin go together")
+    if cos is not None:
+        for n, t in (("cos", cos), ("sin", sin)):
+            _require_cuda_fp16(n, t, 2)
+            if t.shape[0] != t_:
+                raise ValueError(f"{n} must be (T, 64) per-token tables")
+        if cos.stride() != sin.stride():
+            cos, sin = cos.contiguous(), sin.contiguous()
+        cs_sn = cos.stride(0)
+    if (key_cache is None) != (value_cache is None):
+        raise ValueError("key_cache and value_cache go together")
+    cap = 0
+    if key_cache is not None:
+        _require_cuda_fp16("key_cache", key_cache, 4)
+        _require_cuda_fp16("value_cache", value_cache, 4)
+        cap = key_cache.shape[2]
+        if key_cache.shape[:2] != (b, kvh) or value_cache.shape != key_cache.shape:
+            raise ValueError("caches must be (B, KVH, cap, 64)")
+        if start_pos < 0 or start_pos + max_seqlen > cap:
+            raise ValueError("start_pos + max_seqlen exceeds the cache capacity")
+    elif cos is not None:
+        raise ValueError("rotated keys need the caches")
+    out = torch.empty_like(query)
+    kc_s = key_cache.stride()[:3] if key_cache is not None else (0, 0, 0)
+    vc_s = value_cache.stride()[:3] if value_cache is not None else (0, 0, 0)
+    lib = _lib.load()
+    with torch.cuda.device(query.device):
+        rc = lib.qf_prefill_varlen(
+            query.data_ptr(), query.stride(1), query.stride(0),
+            key.data_ptr(), key.stride(1), key.stride(0),
+            value.data_ptr(), value.stride(1), value.stride(0),
+            cu_seqlens.data_ptr(), t_, int(max_seqlen),
+            _ptr(cos), _ptr(sin), cs_sn,
+            _ptr(key_cache), *kc_s, _ptr(value_cache), *vc_s,
+            int(start_pos), cap,
+            out.data_ptr(), out.stride(1), out.stride(0),
+            b, qh, kvh, d, float(d ** -0.5), _stream(query.device))
+    _lib.check(rc, "qf_prefill_varlen")
     return out
 
 

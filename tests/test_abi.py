@@ -142,3 +142,17 @@ def test_prefill_workspace_plan():
                                 None, 0, 0, 0, None, 0, 0, 0, 0, 0, 16, 0, 0, 0,
                                 1, 14, 2, 2048, 64, 0.125, 16, 1024, None)
     assert rc == -1
+
+
+def test_prefill_varlen_rejects_bad_arguments():
+    lib = _lib.load()
+
+    def call(cu=16, total=8, max_seqlen=8, cos=None, sin=None, kc=None, vc=None, cap=0):
+        return lib.qf_prefill_varlen(16, 64, 896, 16, 64, 128, 16, 64, 128, cu, total, max_seqlen,
+                                     cos, sin, 64, kc, 0, 0, 0, vc, 0, 0, 0, 0, cap,
+                                     16, 64, 896, 2, 14, 2, 64, 0.125, None)
+
+    assert call(cu=None) == -1                      # no row offsets
+    assert call(total=0) == -1
+    assert call(cos=16, sin=16) == -2               # RoPE needs the caches
+    assert call(kc=16, vc=16, cap=4) == -1          # max_seqlen exceeds capacity

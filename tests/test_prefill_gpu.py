@@ -119,3 +119,42 @@ def test_split_query_tiles_match_unsplit(dev, seq):
     assert _err(split.cpu(), ref) <= TOL
     assert _err(plain.cpu(), ref) <= TOL
     assert _err(split, plain) <= TOL
+
+
+@pytest.mark.parametrize("lengths", [[1, 65, 200, 513], [130], [64, 64, 7]])
+def test_varlen_prefill_rope_append_matches_per_row_oracle(dev, lengths):
+    """Packed ragged rows (SE:1162-1204 semantics): each row is its own causal
+    prefill at positions 0..len-1, K/V land in slots [0, len) of its cache row,
+    every other slot is untouched."""
+    from oracle.rope import inv_freq, rope_cos_sin
+
+    gen = torch.Generator().manual_seed(sum(lengths))
+    b, total, qh, kvh = len(lengths), sum(lengths), 14, 2
+    q = torch.randn(total, qh, 64, generator=gen).half()
+    k = torch.randn(total, kvh, 64, generator=gen).half()
+    v = torch.randn(total, kvh, 64, generator=gen).half()
+    pos = torch.cat([torch.arange(n) for n in lengths])
+    cos, sin = rope_cos_sin(pos, inv_freq(64, 1e6))
+    starts = [0]
+    for n in lengths:
+        starts.append(starts[-1] + n)
+    cap = (max(lengths) + 63) // 64 * 64 + 64
+    kc0 = torch.randn(b, kvh, cap, 64, generator=gen).half()
+    vc0 = torch.randn(b, kvh, cap, 64, generator=gen).half()
+    kc, vc = kc0.to(dev), vc0.to(dev)
+    cu = torch.tensor(starts, dtype=torch.int32, device=dev)
+    print(f"[prefill varlen] lengths={lengths}", flush=True)
+    out = ops.prefill_varlen(q.to(dev), k.to(dev), v.to(dev), cu, max(lengths), cos.to(dev),
+                             sin.to(dev), kc, vc, 0)
+    torch.cuda.synchronize()
+    out, kc, vc = out.cpu(), kc.cpu(), vc.cpu()
+    for i, n in enumerate(lengths):
+        sl = slice(starts[i], starts[i + 1])
+        q_rot = oracle.apply_rope_fp16(q[sl].transpose(0, 1), cos[sl], sin[sl])   # (QH, n, 64)
+        k_rot = oracle.apply_rope_fp16(k[sl].transpose(0, 1), cos[sl], sin[sl])   # (KVH, n, 64)
+        ref = oracle.causal_prefill(q_rot[None], k_rot[None], v[sl].transpose(0, 1)[None])[0]
+        assert _err(out[sl].transpose(0, 1), ref) <= TOL, f"row {i}"
+        assert torch.equal(kc[i, :, :n], k_rot)
+        assert torch.equal(vc[i, :, :n], v[sl].transpose(0, 1))
+        assert torch.equal(kc[i, :, n:], kc0[i, :, n:])
+        assert torch.equal(vc[i, :, n:], vc0[i, :, n:])
