@@ -263,6 +263,21 @@ def bench_e2e(dev, batches=(1, 4), prefix=1024, new_tokens=128):
             "weight_GBps": round(cfg.weight_bytes() / (timing["decode_ms"] / steps * 1e-3) / 1e9, 1),
         }
         del ids
+    # Ragged batch (the reference's padded-batch path, SE:1241-1335): four
+    # prompts of different lengths, packed prefill, decode over masked holes.
+    lengths = (512, 700, 896, 1024)
+    gen = torch.Generator().manual_seed(7)
+    prompts = [torch.randint(0, cfg.vocab, (n,), generator=gen).to(dev) for n in lengths]
+    eng.generate_ragged(prompts, 8)
+    timing = {}
+    eng.generate_ragged(prompts, new_tokens, timing)
+    steps = new_tokens - 1
+    out["ragged"] = {
+        "lengths": list(lengths),
+        "decode_tok_s": round(len(lengths) * steps / (timing["decode_ms"] * 1e-3), 1),
+        "ms_per_step": round(timing["decode_ms"] / steps, 4),
+        "prefill_ms": round(timing["prefill_ms"], 3),
+    }
     return out
 
 
@@ -408,11 +423,14 @@ def main():
             "splits": lg["splits"],
         }
         bw = {}
-        for b, L in ((16, 32768), (64, 4096)):
+        for b, L in ((12, 5760), (16, 32768), (64, 4096)):
             x = bench_bandwidth_decode(args.steps, args.warmup, dev, b, L)
             gbs_full = x["bytes"] / (x["us_full"] * 1e-6) / 1e9
             gbs_split = x["bytes"] / (x["us_split"] * 1e-6) / 1e9
             bw[f"B{b}_L{L}"] = {
+                **({"note": "the reference's own flash-decode benchmark shape (0.180 ms/layer, "
+                            "~197 GB/s on its RTX 2080 Ti, README.md:61)"}
+                   if (b, L) == (12, 5760) else {}),
                 "us_per_layer": round(x["us_full"], 3),
                 "GBps": round(gbs_full, 1),
                 "hbm_frac": round(gbs_full / HBM_PEAK_GBS, 4),
@@ -442,6 +460,7 @@ def main():
             "prefill_ms_bs1": e2e[1]["prefill_ms"],
             "prefill_ms_bs4": e2e[4]["prefill_ms"],
             "weight_stream_GBps_bs1": e2e[1]["weight_GBps"],
+            "ragged_bs4": e2e["ragged"],
             "workload": "24 layers, hidden 896, 14/2 heads, vocab 151936, random-init fp16 "
                         "(std 0.02), 1024-token random prefix, 128 greedy tokens; "
                         "tok/s = B*127 / graph-replay decode time",
