@@ -60,12 +60,13 @@ struct Args {
   int64_t o_sb, o_sh, o_sn;
   int B, QH, KVH, G, S;
   float scale_log2;
-  // Split-K of the heaviest query tiles (LDS kernel only): query tiles
-  // mt >= split_from run as two workgroups over key tiles [0, split_from) and
-  // [split_from, mt], which write fp32 partials to `part` for the merge
-  // kernel.  n_split = number of split query tiles (0: no split).
+  // Split-K of long query tiles (LDS kernel only): query tile mt, with
+  // n = mt + 1 key tiles, runs as P = ceil(n / split_tiles) workgroups over
+  // equal key-tile ranges; when P > 1 each writes an fp32 partial to `part`
+  // (slot [bq][mt][p], p < max_parts) for the merge kernel.  split_tiles == 0:
+  // no split (one workgroup per query tile).
   float* part;
-  int split_from, n_split;
+  int split_tiles, max_parts;
   // Packed variable-length rows (ragged prefill): row b's tokens are
   // [cu[b], cu[b+1]) of q/k/v/out/cos/sin, whose batch strides are then 0;
   // S holds the longest row.  kv_packed: k/v are those packed inputs (1) or
@@ -358,8 +359,12 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(Args a) {
 // direct-to-LDS loads (global_load_lds) into a three-stage ring, so no
 // registers stage the data and two tiles are always in flight.  LDS rows are
 // 128 bytes, XOR-swizzled in 16-byte chunks (chunk c of row r lives at
-// c ^ swz(r)), which makes both the K operand reads (16 rows x 16 bytes per
-// lane group) and the transposing V reads conflict-free.  V^T operands come
+// c ^ swz(r)).  gfx950's LDS serves 256 bytes per cycle (64 banks of 4
+// bytes: a 16-byte read takes 16 lanes at a time).  With
+// swz(r) = r1 | r3 << 1 | (r1 ^ r4) << 2 (ri = bit i of r) the 16 lanes of a
+// K operand read (rows 8*(c/4) + 4j + c%4, one logical chunk) hit 16
+// distinct 16-byte bank groups, i.e. the reads are conflict-free; a swizzle
+// that breaks this doubles SQ_LDS_BANK_CONFLICT (measured).  V^T operands come
 // from ds_read_b64_tr_b16: within each 16-lane group, lane i receives element
 // i % 4 of the 8-byte words addressed by lanes 4t + i/4 (t = 0..3), so lanes
 // that address 4 keys x 16 dims of V receive V^T[d][4 keys] directly.
@@ -367,7 +372,10 @@ constexpr int kStages = 3;
 constexpr int kRowBytes = kD * 2;  // 128
 constexpr int kPartVals = kD + 2;  // per query row of a split partial: o[64], m, l
 
-__device__ __forceinline__ int swz(int row) { return 2 * ((row >> 3) & 3) + ((row >> 1) & 1); }
+__device__ __forceinline__ int swz(int row) {
+  const int r1 = (row >> 1) & 1, r3 = (row >> 3) & 1, r4 = (row >> 4) & 1;
+  return r1 | (r3 << 1) | ((r1 ^ r4) << 2);
+}
 
 __device__ __forceinline__ void s_waitcnt_vm(int n) {
   // gfx9 encoding: vmcnt[3:0] | expcnt=7 | lgkmcnt=15 | vmcnt[5:4] << 14.
@@ -536,17 +544,26 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_lds_kernel(Args a) {
   __shared__ __attribute__((aligned(16))) unsigned char k1[kBN * kRowBytes], v1[kBN * kRowBytes];
   __shared__ __attribute__((aligned(16))) unsigned char k2[kBN * kRowBytes], v2[kBN * kRowBytes];
 
-  // Work item -> (query tile, key-tile range), heaviest first: the n_split
-  // split query tiles come as pairs (part 0: keys [0, split_from), part 1:
-  // the rest, diagonal included), then the unsplit tiles in falling order.
+  // Work item -> (query tile, part), heaviest query tiles first, the parts of
+  // one query tile consecutive.
   const int n_mtiles = (a.S + kBM - 1) / kBM;
-  const int x = blockIdx.x;
-  int mt, part = -1;
-  if (x < 2 * a.n_split) {
-    mt = n_mtiles - 1 - (x >> 1);
-    part = x & 1;
-  } else {
-    mt = n_mtiles - 1 - a.n_split - (x - 2 * a.n_split);
+  int mt = n_mtiles - 1 - (int)blockIdx.x, part = 0, n_parts = 1;
+  if (a.split_tiles > 0) {
+    // Query tiles [g*T, g*T + T) have g + 1 parts each; walk the groups from
+    // the top (the top group may be partial).
+    const int T = a.split_tiles;
+    int rem = blockIdx.x, hi = n_mtiles - 1;
+    for (;;) {
+      const int g = hi / T, np = g + 1, cnt = hi - g * T + 1;
+      if (rem < cnt * np || g == 0) {
+        mt = hi - rem / np;
+        part = rem % np;
+        n_parts = np;
+        break;
+      }
+      rem -= cnt * np;
+      hi = g * T - 1;
+    }
   }
   const int bq = blockIdx.y;
   const int b = bq / a.QH, hq = bq % a.QH;
@@ -570,10 +587,9 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_lds_kernel(Args a) {
   c.grp = grp;
   c.w = w;
   const int key_end = (mt + 1) * kBM < S ? (mt + 1) * kBM : S;
-  c.n_ktiles = (key_end + kBN - 1) / kBN;  // end of this item's key tiles
-  int kt0 = 0;
-  if (part == 0) c.n_ktiles = a.split_from;
-  if (part == 1) kt0 = a.split_from;
+  const int n_all = (key_end + kBN - 1) / kBN;
+  const int kt0 = part * n_all / n_parts;       // this part's key tiles [kt0, end)
+  c.n_ktiles = (part + 1) * n_all / n_parts;
   c.qrow = mt * kBM + w * 16 + col;
   // Loader mapping: lane -> row 8i + lane/8 of the wave's 16, physical chunk lane % 8.
   c.lrow0 = 16 * w + (lane >> 3);
@@ -636,12 +652,12 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_lds_kernel(Args a) {
   }
 
   const float l_run = c.l4[0];
-  if (part >= 0) {
+  if (n_parts > 1) {
     // Partial of a split query tile: unnormalised o, running max (log2
-    // units) and sum, for the merge kernel.  Layout [bq][split tile][part]
-    // [row][kPartVals]; grp 0 also writes m and l.
-    const int si = n_mtiles - 1 - mt;
-    float* pp = a.part + ((((int64_t)bq * a.n_split + si) * 2 + part) * kBM + w * 16 + col) * kPartVals;
+    // units) and sum, for the merge kernel.  Layout [bq][mt][part][row]
+    // [kPartVals]; grp 0 also writes m and l.
+    float* pp = a.part + ((((int64_t)bq * n_mtiles + mt) * a.max_parts + part) * kBM + w * 16 + col) *
+                             kPartVals;
 #pragma unroll
     for (int t = 0; t < 4; ++t) *reinterpret_cast<f32x4*>(pp + 16 * t + 4 * grp) = c.o[t];
     if (grp == 0) {
@@ -679,34 +695,58 @@ __device__ __forceinline__ void merge_write(const Args& a, int b, int hq, int qr
   *reinterpret_cast<f16x4*>(a.out + b * a.o_sb + hq * a.o_sh + (int64_t)qrow * a.o_sn + 4 * d4) = r;
 }
 
-// Merge of the two partials of each split query tile: grid (n_split, B*QH),
-// four (row, 4 dims) items per thread, every load issued before any use.
+// Merge of the P partials of each split query tile: grid (query tiles that
+// split, B*QH), four (row, 4 dims) items per thread, each part's loads
+// issued together.  o = sum_p o_p s_p / sum_p l_p s_p with s_p = 2^(m_p - m),
+// m = max_p m_p, rounded once to fp16.
 __global__ __launch_bounds__(256) void prefill_merge_kernel(Args a) {
   const int n_mtiles = (a.S + kBM - 1) / kBM;
-  const int si = blockIdx.x, bq = blockIdx.y;
-  const int mt = n_mtiles - 1 - si;
+  const int mt = a.split_tiles + blockIdx.x;  // the first split query tile is split_tiles
+  const int bq = blockIdx.y;
   const int b = bq / a.QH, hq = bq % a.QH;
-  const float* p0 = a.part + (((int64_t)bq * a.n_split + si) * 2) * kBM * kPartVals;
-  const float* p1 = p0 + kBM * kPartVals;
+  const int n_parts = (mt + a.split_tiles) / a.split_tiles;
+  const float* p0 = a.part + ((int64_t)bq * n_mtiles + mt) * a.max_parts * kBM * kPartVals;
   constexpr int kItems = kBM * 16 / 256;
-  f32x4 o0[kItems], o1[kItems];
-  float m0[kItems], l0[kItems], m1[kItems], l1[kItems];
+  float M[kItems], L[kItems];
+  f32x4 O[kItems];
 #pragma unroll
   for (int i = 0; i < kItems; ++i) {
-    const int it = threadIdx.x + 256 * i;
-    const int row = it >> 4, d4 = it & 15;
-    o0[i] = *reinterpret_cast<const f32x4*>(p0 + row * kPartVals + 4 * d4);
-    o1[i] = *reinterpret_cast<const f32x4*>(p1 + row * kPartVals + 4 * d4);
-    m0[i] = p0[row * kPartVals + 64];
-    l0[i] = p0[row * kPartVals + 65];
-    m1[i] = p1[row * kPartVals + 64];
-    l1[i] = p1[row * kPartVals + 65];
+    M[i] = kNegInf;
+    L[i] = 0.f;
+    O[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  for (int p = 0; p < n_parts; ++p) {
+    const float* pp = p0 + (int64_t)p * kBM * kPartVals;
+    f32x4 o[kItems];
+    float m[kItems], l[kItems];
+#pragma unroll
+    for (int i = 0; i < kItems; ++i) {
+      const int it = threadIdx.x + 256 * i;
+      const int row = it >> 4, d4 = it & 15;
+      o[i] = *reinterpret_cast<const f32x4*>(pp + row * kPartVals + 4 * d4);
+      m[i] = pp[row * kPartVals + 64];
+      l[i] = pp[row * kPartVals + 65];
+    }
+#pragma unroll
+    for (int i = 0; i < kItems; ++i) {
+      const float mn = fmaxf(M[i], m[i]);
+      const float s_old = (M[i] == kNegInf) ? 0.f : fast_exp2(M[i] - mn);
+      const float s_new = (m[i] == kNegInf) ? 0.f : fast_exp2(m[i] - mn);
+      L[i] = L[i] * s_old + l[i] * s_new;
+      O[i] = O[i] * s_old + o[i] * s_new;
+      M[i] = mn;
+    }
   }
 #pragma unroll
   for (int i = 0; i < kItems; ++i) {
     const int it = threadIdx.x + 256 * i;
-    const int qrow = mt * kBM + (it >> 4);
-    if (qrow < a.S) merge_write(a, b, hq, qrow, it & 15, o0[i], m0[i], l0[i], o1[i], m1[i], l1[i]);
+    const int qrow = mt * kBM + (it >> 4), d4 = it & 15;
+    if (qrow >= a.S) continue;
+    const float inv = 1.f / L[i];
+    f16x4 r;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) r[c] = (f16)(O[i][c] * inv);
+    *reinterpret_cast<f16x4*>(a.out + b * a.o_sb + hq * a.o_sh + (int64_t)qrow * a.o_sn + 4 * d4) = r;
   }
 }
 
@@ -749,24 +789,35 @@ using namespace qf;
 
 static bool aligned16p(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Query tiles below this count are not split (the chain is already short).
-static constexpr int kSplitMinTiles = 8;
+// Key tiles per split part: query tiles with more key tiles than this run as
+// several workgroups.  Short prompts (fewer query tiles) are not split.
+#ifndef QF_PF_SPLIT_TILES
+#define QF_PF_SPLIT_TILES 16
+#endif
+static constexpr int kSplitTiles = QF_PF_SPLIT_TILES;
 
-static void split_plan(int S, int& split_from, int& n_split) {
+static void split_plan(int S, int& split_tiles, int& max_parts, int& n_items, int& n_merge) {
   const int n_mtiles = (S + qf::prefill::kBM - 1) / qf::prefill::kBM;
-  split_from = 0;
-  n_split = 0;
-  if (n_mtiles < kSplitMinTiles) return;
-  split_from = (n_mtiles + 1) / 2;
-  n_split = n_mtiles - split_from;
+  split_tiles = 0;
+  max_parts = 1;
+  n_items = n_mtiles;
+  n_merge = 0;
+  if (n_mtiles <= kSplitTiles) return;
+  split_tiles = kSplitTiles;
+  max_parts = (n_mtiles + kSplitTiles - 1) / kSplitTiles;
+  n_items = 0;
+  for (int mt = 0; mt < n_mtiles; ++mt) n_items += (mt + kSplitTiles) / kSplitTiles;
+  n_merge = n_mtiles - kSplitTiles;
 }
 
 extern "C" int64_t qf_prefill_workspace_bytes(int B, int QH, int S) {
   using namespace qf::prefill;
   if (B < 1 || QH < 1 || S < 1) return 0;
-  int split_from, n_split;
-  split_plan(S, split_from, n_split);
-  return (int64_t)B * QH * n_split * 2 * kBM * kPartVals * (int64_t)sizeof(float);
+  int split_tiles, max_parts, n_items, n_merge;
+  split_plan(S, split_tiles, max_parts, n_items, n_merge);
+  if (n_merge == 0) return 0;
+  const int n_mtiles = (S + kBM - 1) / kBM;
+  return (int64_t)B * QH * n_mtiles * max_parts * kBM * kPartVals * (int64_t)sizeof(float);
 }
 
 extern "C" int qf_prefill_attn(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sn,
@@ -816,11 +867,16 @@ static int prefill_launch(Args a, bool rope, bool append, hipStream_t st) {
     a.v_sb = a.vc_sb; a.v_sh = a.vc_sh; a.v_sn = a.vc_sn;
     a.kv_packed = 0;
   }
-  const dim3 lgrid(grid.x + a.n_split, B * QH);
+  int n_items = grid.x, n_merge = 0;
+  if (a.split_tiles > 0) {
+    int st_, mp_;
+    split_plan(S, st_, mp_, n_items, n_merge);
+  }
+  const dim3 lgrid(n_items, B * QH);
   if (rope) hipLaunchKernelGGL((prefill_lds_kernel<true>), lgrid, block, 0, st, a);
   else hipLaunchKernelGGL((prefill_lds_kernel<false>), lgrid, block, 0, st, a);
-  if (a.n_split > 0)
-    hipLaunchKernelGGL(prefill_merge_kernel, dim3(a.n_split, B * QH), dim3(256), 0, st, a);
+  if (n_merge > 0)
+    hipLaunchKernelGGL(prefill_merge_kernel, dim3(n_merge, B * QH), dim3(256), 0, st, a);
   return (int)hipGetLastError();
 }
 
@@ -859,8 +915,8 @@ static int fill_common(Args& a, const void* q, const void* k, const void* v, con
   a.B = B; a.QH = QH; a.KVH = KVH; a.G = QH / KVH; a.S = S;
   a.scale_log2 = scale * kLog2e;
   a.part = nullptr;
-  a.split_from = 0;
-  a.n_split = 0;
+  a.split_tiles = 0;
+  a.max_parts = 1;
   a.cu = nullptr;
   a.total = 0;
   a.kv_packed = 1;
@@ -896,7 +952,8 @@ extern "C" int qf_prefill_attn_ws(const void* q, int64_t q_sb, int64_t q_sh, int
     if (!aligned16p(workspace) || workspace_bytes < qf_prefill_workspace_bytes(B, QH, S))
       return QF_ERR_INVALID_ARG;
     a.part = static_cast<float*>(workspace);
-    split_plan(S, a.split_from, a.n_split);
+    int n_items, n_merge;
+    split_plan(S, a.split_tiles, a.max_parts, n_items, n_merge);
   }
   return prefill_launch(a, rope, append, static_cast<hipStream_t>(stream));
 }
