@@ -399,6 +399,11 @@ struct LdsCtx {
   const f16* vb;
   int kvo[2];         // byte offset, within a tile, of this lane's two K rows' chunk
   int vvo[2];         // same for V
+  // Next tile to issue (tiles are issued in increasing order): its first K/V
+  // byte and the valid bytes from there to the end of the sequence.
+  const unsigned char* knext;
+  const unsigned char* vnext;
+  int64_t krem, vrem;
   int64_t k_sn, v_sn;
   int S, mt, qrow, n_ktiles, grp, lrow0, pch, w;
   int koff[2][2][2];  // [ch][j][kk] LDS byte offsets of the K operand reads
@@ -409,25 +414,21 @@ struct LdsCtx {
   f32x4 o[4];
 };
 
-// Buffer resource over the rows [key0, S) of a K or V head (row stride sn
-// elements): the tile's base address and valid byte count live in SGPRs, so
-// a lane's load offset within the tile never changes, and rows past the
-// sequence (the last tile's tail) read as zero (their scores are masked).
-// Needs sn >= 64 so the last row's 128 bytes lie below the record count.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const f16* head, int64_t sn, int key0,
-                                                            int S) {
-  const int64_t bytes = (int64_t)(S - key0) * sn * 2;
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(head + key0 * sn), (short)0,
-                                           (int)(bytes < 0x7fffffff ? bytes : 0x7fffffff),
-                                           0x00020000);
+// Buffer resource over `rem` valid bytes from `base` (a tile's first row):
+// the tile's address and valid byte count live in SGPRs, so a lane's load
+// offset within the tile never changes, and rows past the sequence (the last
+// tile's tail) read as zero (their scores are masked).  Needs row strides
+// >= 64 elements so a row's 128 bytes lie below the record count.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const unsigned char* base, int64_t rem) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(base), (short)0,
+                                           (int)(rem < 0x7fffffff ? rem : 0x7fffffff), 0x00020000);
 }
 
-// Async loads of tile kt (this wave's 16 rows of K and of V) into (Kd, Vd).
-__device__ __forceinline__ void lds_issue(const LdsCtx& c, int kt, unsigned char* Kd,
-                                          unsigned char* Vd) {
-  const int key0 = kt * kBN;
-  const __amdgpu_buffer_rsrc_t rk = tile_rsrc(c.kb, c.k_sn, key0, c.S);
-  const __amdgpu_buffer_rsrc_t rv = tile_rsrc(c.vb, c.v_sn, key0, c.S);
+// Async loads of the next tile (this wave's 16 rows of K and of V) into
+// (Kd, Vd); advances the issue cursor by one tile (scalar adds only).
+__device__ __forceinline__ void lds_issue(LdsCtx& c, unsigned char* Kd, unsigned char* Vd) {
+  const __amdgpu_buffer_rsrc_t rk = tile_rsrc(c.knext, c.krem);
+  const __amdgpu_buffer_rsrc_t rv = tile_rsrc(c.vnext, c.vrem);
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(Kd + (16 * c.w + 8 * i) * kRowBytes),
@@ -435,6 +436,11 @@ __device__ __forceinline__ void lds_issue(const LdsCtx& c, int kt, unsigned char
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)(Vd + (16 * c.w + 8 * i) * kRowBytes),
                                              16, c.vvo[i], 0, 0, 0);
   }
+  const int64_t kstep = kBN * c.k_sn * 2, vstep = kBN * c.v_sn * 2;
+  c.knext += kstep;
+  c.vnext += vstep;
+  c.krem -= kstep;
+  c.vrem -= vstep;
 }
 
 // v_max3_f32 on raw registers.  fmaxf would first canonicalise every MFMA
@@ -481,7 +487,7 @@ __device__ __forceinline__ void lds_step(LdsCtx& c, int kt, const unsigned char*
       for (int kk = 0; kk < 2; ++kk)
         ka[ch][j][kk] = *reinterpret_cast<const f16x8*>(Ks + c.koff[ch][j][kk]);
   // Refill after the K operands are in registers (the V^T reads come later).
-  if (kt + 2 < c.n_ktiles) lds_issue(c, kt + 2, Kn, Vn);
+  if (kt + 2 < c.n_ktiles) lds_issue(c, Kn, Vn);  // tile kt + 2
   f32x4 sc[4];
 #pragma unroll
   for (int ch = 0; ch < 2; ++ch)
@@ -617,8 +623,12 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_lds_kernel(Args a) {
       qcs[3] = load16(a.sin + co + 32);
     }
   }
-  lds_issue(c, kt0, k0, v0);
-  if (kt0 + 1 < c.n_ktiles) lds_issue(c, kt0 + 1, k1, v1);
+  c.knext = reinterpret_cast<const unsigned char*>(c.kb + (int64_t)kt0 * kBN * c.k_sn);
+  c.vnext = reinterpret_cast<const unsigned char*>(c.vb + (int64_t)kt0 * kBN * c.v_sn);
+  c.krem = (int64_t)(S - kt0 * kBN) * c.k_sn * 2;
+  c.vrem = (int64_t)(S - kt0 * kBN) * c.v_sn * 2;
+  lds_issue(c, k0, v0);                                // tile kt0
+  if (kt0 + 1 < c.n_ktiles) lds_issue(c, k1, v1);      // tile kt0 + 1
   if (kRopeQ) rope_pair(c.qf[0], c.qf[1], qcs[0], qcs[1], qcs[2], qcs[3]);
 
 #pragma unroll
