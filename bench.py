@@ -406,7 +406,7 @@ def main():
             "unit": "GB/s",
             "frac": round(split_gbs / HBM_PEAK_GBS, 4),
             "traffic": _traffic(),
-            "kernel": "qf::decode_split_kernel<8, 1, 1> (qf_decode_split: 8 waves, vector bias, partial mode)",
+            "kernel": "qf::decode_split_kernel<8, 1, 1, false> (qf_decode_split: 8 waves, vector bias, partial mode, dense cache)",
             "bytes_per_launch": int(launch_bytes),
             "avg_launch_us": round(us_split, 3),
             "combine_kernel_avg_us": (None if r["ms_combine"] is None

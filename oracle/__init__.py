@@ -21,6 +21,9 @@ make the restatement trustworthy live in ``tests/test_oracle_*.py``:
   arithmetic (two independent correctly-rounded implementations), position-0
   identity, fp64 norm preservation, and the whiteboard split-half KAT.
 * ``append_*`` / ``capacity`` / ``decode_slots``: brute-force loops.
+* ``pages_to_dense`` / ``dense_to_pages`` / ``paged_location``: the identity
+  block table reduces to a reshape of the dense cache (closed form), and the
+  two are inverse on random tables.
 
 No function is "parity unpinned".
 """
@@ -43,7 +46,11 @@ from .rope import (  # noqa: F401
 from .kv import (  # noqa: F401
     append_decode,
     append_prefill,
+    append_rows,
     capacity,
+    dense_to_pages,
+    pages_to_dense,
+    paged_location,
     decode_bias,
     decode_slots,
 )

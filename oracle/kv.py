@@ -60,3 +60,52 @@ def decode_bias(lengths, max_prompt_len: int, cap: int, steps_done: int) -> torc
         bias[b, :n] = 0.0
         bias[b, max_prompt_len:max_prompt_len + steps_done] = 0.0
     return bias
+
+
+# --------------------------------------------------------------------------
+# Paged layout (block table).  The reference keeps dense (B, KVH, cap, D)
+# caches and lists block-level KV management only as a roadmap item
+# (README.md:144), so this is the data contract of the paged kernels stated
+# as plain indexing: logical slot s of row b lives in
+# pool[table[b, s // P], :, s % P].
+# --------------------------------------------------------------------------
+
+def paged_location(table, b: int, slot: int, page_size: int):
+    """(physical page, row in page) of logical slot ``slot`` of row ``b``."""
+    return int(table[b, slot // page_size]), slot % page_size
+
+
+def pages_to_dense(pool, table, lengths, cap: int):
+    """Gather a paged pool (n_pages, KVH, P, D) into a dense (B, KVH, cap, D)
+    cache: slots below ``lengths[b]`` come from the pages, the rest are zero
+    (the dense caches are zero-initialised, SE:705-714)."""
+    n_pages, kvh, page, d = pool.shape
+    dense = torch.zeros(len(lengths), kvh, cap, d, dtype=pool.dtype)
+    for b, n in enumerate(lengths):
+        for s in range(n):
+            p, r = paged_location(table, b, s, page)
+            dense[b, :, s] = pool[p, :, r]
+    return dense
+
+
+def dense_to_pages(dense, table, lengths, n_pages: int, page_size: int):
+    """Scatter slots ``[0, lengths[b])`` of a dense cache into a fresh zero pool."""
+    b_, kvh, cap, d = dense.shape
+    pool = torch.zeros(n_pages, kvh, page_size, d, dtype=dense.dtype)
+    for b, n in enumerate(lengths):
+        for s in range(n):
+            p, r = paged_location(table, b, s, page_size)
+            pool[p, :, r] = dense[b, :, s]
+    return pool
+
+
+def append_rows(key_cache, value_cache, key, value, slots):
+    """Per-row decode append (each row at its own slot; a slot outside
+    [0, cap) writes nothing): the no-holes form of SE:930-932 that a paged
+    batch uses.  key/value (B, KVH, 1, D); caches updated in place."""
+    cap = key_cache.shape[2]
+    for b, s in enumerate(int(x) for x in slots):
+        if 0 <= s < cap:
+            key_cache[b, :, s] = key[b, :, 0]
+            value_cache[b, :, s] = value[b, :, 0]
+    return key_cache, value_cache

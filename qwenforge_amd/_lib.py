@@ -1,4 +1,5 @@
-"""ctypes binding of the C ABI in ``include/qf_attn.h`` and ``include/qf_step.h``.
+"""ctypes binding of the C ABI in ``include/qf_attn.h``, ``include/qf_step.h`` and
+``include/qf_paged.h``.
 
 The shared object is built in-tree by ``qwenforge_amd.build``.  There is no
 fallback: if it is missing or does not load, every op raises.
@@ -138,6 +139,72 @@ SIGNATURES = {
         _vp, _i32, _i32, _vp,           # keys, n_blocks, B, token
         _vp, _i64, _i32,                # rows, rows_sb, n_rows
         _vp, _vp, _vp,                  # step, write_index, pos
+        _vp,                            # stream
+    ],
+    # include/qf_paged.h
+    "qf_decode_attn_paged": [
+        _vp, _i64, _i64, _i64,          # q, q_sb, q_sh, q_sg
+        _vp, _i64, _i64, _i64,          # k_pool, kp_sp, kp_sh, kp_sn
+        _vp, _i64, _i64, _i64,          # v_pool, vp_sp, vp_sh, vp_sn
+        _vp, _i64, _i32, _i32, _i32,    # block_table, bt_sb, pages_per_row, n_pages, page_size
+        _vp, _i64,                      # bias, bias_sb
+        _vp, _i64,                      # kv_last, kv_last_sb
+        _vp, _vp, _vp, _i32,            # acc, m, l, splits
+        _vp,                            # ticket
+        _vp, _i64, _i64, _i64,          # out, o_sb, o_sh, o_sg
+        _i32, _i32, _i32, _i32,         # B, KVH, G, D
+        _f32, _vp,                      # scale, stream
+    ],
+    "qf_decode_split_paged": [
+        _vp, _i64, _i64, _i64,          # q
+        _vp, _i64, _i64, _i64,          # k_pool
+        _vp, _i64, _i64, _i64,          # v_pool
+        _vp, _i64, _i32, _i32, _i32,    # block_table, bt_sb, pages_per_row, n_pages, page_size
+        _vp, _i64,                      # bias, bias_sb
+        _vp, _i64,                      # kv_last, kv_last_sb
+        _vp, _vp, _vp, _i32,            # acc, m, l, splits
+        _i32, _i32, _i32, _i32,         # B, KVH, G, D
+        _f32, _vp,                      # scale, stream
+    ],
+    "qf_rope_append_paged": [
+        _vp, _i64, _i64,                # q, q_sb, q_sh
+        _vp, _i64, _i64,                # k
+        _vp, _i64, _i64,                # v
+        _vp, _vp, _i64,                 # cos, sin, cs_sb
+        _vp, _i64, _i64, _i64,          # k_pool
+        _vp, _i64, _i64, _i64,          # v_pool
+        _vp, _i64, _i32, _i32, _i32,    # block_table, bt_sb, pages_per_row, n_pages, page_size
+        _vp, _i64,                      # slots, slot_sb
+        _vp, _i64, _i64,                # q_out
+        _i32, _i32, _i32, _i32,         # B, QH, KVH, D
+        _vp,                            # stream
+    ],
+    "qf_prefill_varlen_paged": [
+        _vp, _i64, _i64,                # q, q_sh, q_sn
+        _vp, _i64, _i64,                # k
+        _vp, _i64, _i64,                # v
+        _vp, _i32, _i32,                # cu_seqlens, total, max_seqlen
+        _vp, _vp, _i64,                 # cos, sin, cs_sn
+        _vp, _i64, _i64, _i64,          # k_pool
+        _vp, _i64, _i64, _i64,          # v_pool
+        _vp, _i64, _i32, _i32, _i32,    # block_table, bt_sb, pages_per_row, n_pages, page_size
+        _i64,                           # start_pos
+        _vp, _i64, _i64,                # out, o_sh, o_sn
+        _i32, _i32, _i32, _i32,         # B, QH, KVH, D
+        _f32, _vp,                      # scale, stream
+    ],
+    "qf_rms_qkv_rope_append_paged": [
+        _vp, _i64, _vp,                 # x, x_sb, token
+        _vp, _i64,                      # hidden_out, ho_sb
+        _vp, _f32,                      # norm_w, eps
+        _vp, _vp,                       # w_qkv, bias
+        _vp, _vp, _i64,                 # cos, sin, cs_sb
+        _vp, _i64, _i64, _i64,          # k_pool
+        _vp, _i64, _i64, _i64,          # v_pool
+        _vp, _i64, _i32, _i32, _i32,    # block_table, bt_sb, pages_per_row, n_pages, page_size
+        _vp, _i64,                      # slots, slot_sb
+        _vp, _i64, _i64,                # q_out, qo_sb, qo_sh
+        _i32, _i32, _i32, _i32, _i32,   # B, hidden, QH, KVH, D
         _vp,                            # stream
     ],
     "qf_error_string": [_i32],

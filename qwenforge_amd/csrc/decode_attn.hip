@@ -34,6 +34,7 @@
 // workgroup, so each level costs one dependent memory round trip.
 #include "qf_common.h"
 #include "../../include/qf_attn.h"
+#include "../../include/qf_paged.h"
 
 namespace qf {
 
@@ -65,6 +66,12 @@ struct DecodeArgs {
   int B, KVH, G, cap, splits;
   int bias_vec;      // bias rows 16-byte aligned and cap % 8 == 0: 8 keys per load
   float scale_log2;  // scale * log2(e)
+  // Paged caches: k/v are page pools (n_pages, KVH, P, D) with page strides
+  // k_sp/v_sp (k_sb/v_sb unused); logical slot s of row b lives in page
+  // table[b * t_sb + (s >> log2p)] at row s & (P - 1).  cap = pages per row * P.
+  const int32_t* table;
+  int64_t t_sb, k_sp, v_sp;
+  int log2p, n_pages;
 };
 
 // Partial-scratch accesses.  kCoherent: relaxed agent-scope atomics, which
@@ -236,7 +243,14 @@ __device__ __forceinline__ void load_tile(Tile& t, const f16* kb, const f16* vb,
   }
 }
 
-template <int NW, int kBias, int kMode>
+// Physical page of slot `slot` of row b, clamped into the pool (a page id
+// outside [0, n_pages) is a caller error; clamping keeps the reads in bounds).
+__device__ __forceinline__ int page_of(const DecodeArgs& a, int b, int slot) {
+  const int p = a.table[(int64_t)b * a.t_sb + (slot >> a.log2p)];
+  return min(max(p, 0), a.n_pages - 1);
+}
+
+template <int NW, int kBias, int kMode, bool kPaged>
 __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
   constexpr bool kHasBias = kBias != kNoBias;
   constexpr int NT = NW * 64;
@@ -256,7 +270,8 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
   const int bh = blockIdx.y;
   const int b = bh / a.KVH, h = bh % a.KVH;
   const int tid = threadIdx.x;
-  const int lane = tid & 63, w = tid >> 6;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: tile math stays scalar
   const int col = lane & 15;  // query column / A-operand row
   const int grp = lane >> 4;  // 8-wide k chunk of the operands
 
@@ -292,12 +307,44 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
   f16(*vt)[kVtStride] = reinterpret_cast<f16(*)[kVtStride]>(lds_raw + w * kD * kVtStride * 2);
   const int last = hi - 1;
 
+  // Paged caches: lane j holds the physical page of this wave's tile
+  // win + j (tile i of the wave starts at lo + (w + i*NW) * kTile and lies in
+  // one page, since pages hold a multiple of kTile slots and tiles start on
+  // kTile boundaries); one load per 64 tiles of the wave.  The tile's base
+  // pointers are then shifted so that logical slot numbers index them.
+  int pid = 0;
+  const auto load_pids = [&](int win) {
+    int t = lo + (w + (win + lane) * NW) * kTile;
+    t = t < last ? t : last;
+    pid = page_of(a, b, t > 0 ? t : 0);
+  };
+  const auto tile_base = [&](int i, int t0, const f16*& kt, const f16*& vtb) {
+    if (!kPaged) {
+      kt = kb;
+      vtb = vb;
+      return;
+    }
+    const int page = __builtin_amdgcn_readlane(pid, i & 63);
+    const int64_t first = (int64_t)(t0 & ~((1 << a.log2p) - 1));  // first slot of the page
+    kt = a.k + (int64_t)page * a.k_sp + h * a.k_sh - first * a.k_sn;
+    vtb = a.v + (int64_t)page * a.v_sp + h * a.v_sh - first * a.v_sn;
+  };
+
   int t0 = lo + w * kTile;
   Tile cur, nxt;
-  if (t0 < hi) load_tile<kBias>(cur, kb, vb, biasb, a.k_sn, a.v_sn, t0, last, a.cap, lane);
-  for (; t0 < hi; t0 += NW * kTile) {
+  const f16 *kt_, *vt_;
+  if (kPaged && t0 < hi) load_pids(0);
+  if (t0 < hi) {
+    tile_base(0, t0, kt_, vt_);
+    load_tile<kBias>(cur, kt_, vt_, biasb, a.k_sn, a.v_sn, t0, last, a.cap, lane);
+  }
+  for (int i = 0; t0 < hi; t0 += NW * kTile, ++i) {
     const int tn = t0 + NW * kTile;
-    if (tn < hi) load_tile<kBias>(nxt, kb, vb, biasb, a.k_sn, a.v_sn, tn, last, a.cap, lane);
+    if (tn < hi) {
+      if (kPaged && ((i + 1) & 63) == 0) load_pids(i + 1);
+      tile_base(i + 1, tn, kt_, vt_);
+      load_tile<kBias>(nxt, kt_, vt_, biasb, a.k_sn, a.v_sn, tn, last, a.cap, lane);
+    }
 
     // Bias of the lane's 8 keys t0 + 8*grp + jj, in log2 units.
     float bv[8];
@@ -442,19 +489,22 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
   merge_parts<256, false>(a, bh, q, 1, 0, 1, a.splits, true, lds);
 }
 
-template <int NW, int kBias>
+template <int NW, int kBias, bool kPaged>
 static void launch_split(const DecodeArgs& a, int mode, dim3 grid, hipStream_t st) {
   const dim3 block(NW * 64);
-  if (mode == kDirect) hipLaunchKernelGGL((decode_split_kernel<NW, kBias, kDirect>), grid, block, 0, st, a);
-  else if (mode == kPartial) hipLaunchKernelGGL((decode_split_kernel<NW, kBias, kPartial>), grid, block, 0, st, a);
-  else hipLaunchKernelGGL((decode_split_kernel<NW, kBias, kFused>), grid, block, 0, st, a);
+  if (mode == kDirect)
+    hipLaunchKernelGGL((decode_split_kernel<NW, kBias, kDirect, kPaged>), grid, block, 0, st, a);
+  else if (mode == kPartial)
+    hipLaunchKernelGGL((decode_split_kernel<NW, kBias, kPartial, kPaged>), grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL((decode_split_kernel<NW, kBias, kFused, kPaged>), grid, block, 0, st, a);
 }
 
-template <int NW>
+template <int NW, bool kPaged>
 static void launch_nw(const DecodeArgs& a, int mode, dim3 grid, hipStream_t st) {
-  if (!a.bias) launch_split<NW, kNoBias>(a, mode, grid, st);
-  else if (a.bias_vec) launch_split<NW, kBiasVec>(a, mode, grid, st);
-  else launch_split<NW, kBiasScalar>(a, mode, grid, st);
+  if (!a.bias) launch_split<NW, kNoBias, kPaged>(a, mode, grid, st);
+  else if (a.bias_vec) launch_split<NW, kBiasVec, kPaged>(a, mode, grid, st);
+  else launch_split<NW, kBiasScalar, kPaged>(a, mode, grid, st);
 }
 
 }  // namespace qf
@@ -515,15 +565,26 @@ static int make_args(DecodeArgs& a, const void* q, int64_t q_sb, int64_t q_sh, i
   a.o_sb = o_sb; a.o_sh = o_sh; a.o_sg = o_sg;
   a.B = B; a.KVH = KVH; a.G = G; a.cap = cap; a.splits = splits;
   a.scale_log2 = scale * kLog2e;
+  a.table = nullptr;
+  a.t_sb = a.k_sp = a.v_sp = 0;
+  a.log2p = 0;
+  a.n_pages = 0;
   return QF_OK;
 }
 
-static void launch_split_mode(const DecodeArgs& a, int mode, hipStream_t st) {
+
+template <bool kPaged>
+static void launch_split_paging(const DecodeArgs& a, int mode, hipStream_t st) {
   const dim3 grid(a.splits, a.B * a.KVH);
   const int nw = pick_waves(a.splits, a.B, a.KVH);
-  if (nw == 16) launch_nw<16>(a, mode, grid, st);
-  else if (nw == 8) launch_nw<8>(a, mode, grid, st);
-  else launch_nw<4>(a, mode, grid, st);
+  if (nw == 16) launch_nw<16, kPaged>(a, mode, grid, st);
+  else if (nw == 8) launch_nw<8, kPaged>(a, mode, grid, st);
+  else launch_nw<4, kPaged>(a, mode, grid, st);
+}
+
+static void launch_split_mode(const DecodeArgs& a, int mode, hipStream_t st) {
+  if (a.table != nullptr) launch_split_paging<true>(a, mode, st);
+  else launch_split_paging<false>(a, mode, st);
 }
 
 static void launch_combine(const DecodeArgs& a, hipStream_t st) {
@@ -579,5 +640,69 @@ extern "C" int qf_decode_combine(const float* acc, const float* m, const float* 
                            G, D, 1, 1.f, false, true);
   if (rc != QF_OK) return rc;
   launch_combine(a, static_cast<hipStream_t>(stream));
+  return (int)hipGetLastError();
+}
+
+// Paged variants: the contiguous (B, KVH, cap, D) cache is replaced by page
+// pools and a block table; everything else is the contiguous entry points'.
+static int make_paged(DecodeArgs& a, int64_t kp_sp, int64_t vp_sp, const int32_t* block_table,
+                      int64_t bt_sb, int pages_per_row, int n_pages, int page_size) {
+  const int l2 = page_log2(page_size, pages_per_row, n_pages);
+  if (l2 < 0) return QF_ERR_UNSUPPORTED;
+  if (!block_table || bt_sb < pages_per_row) return QF_ERR_INVALID_ARG;
+  if ((kp_sp | vp_sp) & 7) return QF_ERR_INVALID_ARG;
+  a.table = block_table;
+  a.t_sb = bt_sb;
+  a.k_sp = kp_sp;
+  a.v_sp = vp_sp;
+  a.log2p = l2;
+  a.n_pages = n_pages;
+  return QF_OK;
+}
+
+extern "C" int qf_decode_attn_paged(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sg,
+                                    const void* k_pool, int64_t kp_sp, int64_t kp_sh, int64_t kp_sn,
+                                    const void* v_pool, int64_t vp_sp, int64_t vp_sh, int64_t vp_sn,
+                                    const int32_t* block_table, int64_t bt_sb, int pages_per_row,
+                                    int n_pages, int page_size,
+                                    const void* bias, int64_t bias_sb,
+                                    const int64_t* kv_last, int64_t kv_last_sb,
+                                    float* acc, float* m, float* l, int splits,
+                                    int32_t* ticket,
+                                    void* out, int64_t o_sb, int64_t o_sh, int64_t o_sg,
+                                    int B, int KVH, int G, int D, float scale, void* stream) {
+  if (page_log2(page_size, pages_per_row, n_pages) < 0) return QF_ERR_UNSUPPORTED;
+  DecodeArgs a;
+  int rc = make_args(a, q, q_sb, q_sh, q_sg, k_pool, 0, kp_sh, kp_sn, v_pool, 0, vp_sh, vp_sn,
+                     bias, bias_sb, kv_last, kv_last_sb, acc, m, l, splits, ticket, out, o_sb,
+                     o_sh, o_sg, B, KVH, G, D, pages_per_row * page_size, scale, true, true);
+  if (rc == QF_OK)
+    rc = make_paged(a, kp_sp, vp_sp, block_table, bt_sb, pages_per_row, n_pages, page_size);
+  if (rc != QF_OK) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int mode = splits == 1 ? kDirect : (ticket != nullptr ? kFused : kPartial);
+  launch_split_mode(a, mode, st);
+  if (mode == kPartial) launch_combine(a, st);
+  return (int)hipGetLastError();
+}
+
+extern "C" int qf_decode_split_paged(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sg,
+                                     const void* k_pool, int64_t kp_sp, int64_t kp_sh, int64_t kp_sn,
+                                     const void* v_pool, int64_t vp_sp, int64_t vp_sh, int64_t vp_sn,
+                                     const int32_t* block_table, int64_t bt_sb, int pages_per_row,
+                                     int n_pages, int page_size,
+                                     const void* bias, int64_t bias_sb,
+                                     const int64_t* kv_last, int64_t kv_last_sb,
+                                     float* acc, float* m, float* l, int splits,
+                                     int B, int KVH, int G, int D, float scale, void* stream) {
+  if (page_log2(page_size, pages_per_row, n_pages) < 0) return QF_ERR_UNSUPPORTED;
+  DecodeArgs a;
+  int rc = make_args(a, q, q_sb, q_sh, q_sg, k_pool, 0, kp_sh, kp_sn, v_pool, 0, vp_sh, vp_sn,
+                     bias, bias_sb, kv_last, kv_last_sb, acc, m, l, splits, nullptr, nullptr, 0,
+                     0, 0, B, KVH, G, D, pages_per_row * page_size, scale, true, false);
+  if (rc == QF_OK)
+    rc = make_paged(a, kp_sp, vp_sp, block_table, bt_sb, pages_per_row, n_pages, page_size);
+  if (rc != QF_OK) return rc;
+  launch_split_mode(a, kPartial, static_cast<hipStream_t>(stream));
   return (int)hipGetLastError();
 }

@@ -23,6 +23,7 @@
 // mapping and rounding.
 #include "qf_common.h"
 #include "../../include/qf_step.h"
+#include "../../include/qf_paged.h"
 
 namespace qf {
 namespace step {
@@ -222,10 +223,18 @@ struct QkvArgs {
   f16* q_out;
   int64_t qo_sb, qo_sh;
   int K, QH, KVH, cap, n_pairs;
+  // Paged caches: kc/vc are page pools (page strides kc_sb/vc_sb); row b
+  // appends at logical slot slots[b * slot_sb], in page
+  // table[b * t_sb + (slot >> log2p)].  cap = pages per row << log2p.
+  const int32_t* table;
+  int64_t t_sb;
+  int log2p, n_pages;
+  const int64_t* slots;
+  int64_t slot_sb;
 };
 
 // One wave per (head, d) rotate-half pair: rows head*64 + d and head*64 + d + 32.
-template <int NB>
+template <int NB, bool kPaged>
 __global__ __launch_bounds__(kNT) void rms_qkv_rope_append_kernel(QkvArgs a) {
   constexpr int NS = kMaxNormK / 8 / 64;  // 2
   __shared__ __attribute__((aligned(16))) f16 xs[NB * kMaxNormK];
@@ -247,7 +256,7 @@ __global__ __launch_bounds__(kNT) void rms_qkv_rope_append_kernel(QkvArgs a) {
   // Epilogue operands, loaded now so their latency hides under the weights':
   // lane b < NB finishes batch row b.
   const int be = lane < NB ? lane : 0;
-  const int64_t slot = a.write_index[0];
+  const int64_t slot = kPaged ? a.slots[be * a.slot_sb] : a.write_index[0];
   const float bias0 = a.bias != nullptr ? (float)a.bias[r0] : 0.f;
   const float bias1 = a.bias != nullptr ? (float)a.bias[r1] : 0.f;
   const f16* cp = a.cos + be * a.cs_sb;
@@ -257,6 +266,21 @@ __global__ __launch_bounds__(kNT) void rms_qkv_rope_append_kernel(QkvArgs a) {
   f16x8 w0[NS], w1[NS];
   load_row<NS>(a.w + (int64_t)r0 * K, C, w0, lane);
   load_row<NS>(a.w + (int64_t)r1 * K, C, w1, lane);
+  // Element offsets of the destination slot (kv head 0); the page lookup
+  // (paged caches) depends on the slot, so it is issued after the weights.
+  bool in_range = slot >= 0 && slot < a.cap;
+  int64_t kro, vro;
+  if (kPaged) {
+    const int64_t sl = in_range ? slot : 0;  // branch-free table read
+    const int page = a.table[be * a.t_sb + (sl >> a.log2p)];
+    in_range = in_range && page >= 0 && page < a.n_pages;
+    const int64_t row = sl & ((1 << a.log2p) - 1);
+    kro = (int64_t)page * a.kc_sb + row * a.kc_sn;
+    vro = (int64_t)page * a.vc_sb + row * a.vc_sn;
+  } else {
+    kro = be * a.kc_sb + slot * a.kc_sn;
+    vro = be * a.vc_sb + slot * a.vc_sn;
+  }
   f16* raw = (a.token != nullptr && blockIdx.x == 0) ? a.hidden_out : nullptr;
   rms_finish<NB>(st, K, a.eps, xs, red, raw, a.ho_sb);
   if (!valid) return;
@@ -279,7 +303,6 @@ __global__ __launch_bounds__(kNT) void rms_qkv_rope_append_kernel(QkvArgs a) {
   for (int bb = 1; bb < NB; ++bb)
     if (b == bb) { v0 = s0[bb]; v1 = s1[bb]; }
   const float lo = (float)(f16)(v0 + bias0), hi = (float)(f16)(v1 + bias1);
-  const bool in_range = slot >= 0 && slot < a.cap;
   if (head < a.QH + a.KVH) {
     f16 olo, ohi;
     rope1(lo, hi, cos_lo, sin_lo, cos_hi, sin_hi, olo, ohi);
@@ -288,12 +311,12 @@ __global__ __launch_bounds__(kNT) void rms_qkv_rope_append_kernel(QkvArgs a) {
       q[dd] = olo;
       q[dd + 32] = ohi;
     } else if (in_range) {
-      f16* k = a.kc + b * a.kc_sb + (head - a.QH) * a.kc_sh + slot * a.kc_sn;
+      f16* k = a.kc + kro + (head - a.QH) * a.kc_sh;
       k[dd] = olo;
       k[dd + 32] = ohi;
     }
   } else if (in_range) {
-    f16* v = a.vc + b * a.vc_sb + (head - a.QH - a.KVH) * a.vc_sh + slot * a.vc_sn;
+    f16* v = a.vc + vro + (head - a.QH - a.KVH) * a.vc_sh;
     v[dd] = (f16)lo;
     v[dd + 32] = (f16)hi;
   }
@@ -731,6 +754,7 @@ extern "C" int qf_rms_qkv_rope_append(const void* x, int64_t x_sb, const int64_t
     return QF_ERR_INVALID_ARG;
   if (!al16(x) || !al16(norm_w) || !al16(w_qkv) || (x_sb & 7)) return QF_ERR_INVALID_ARG;
   QkvArgs a;
+  a.table = nullptr; a.t_sb = 0; a.log2p = 0; a.n_pages = 0; a.slots = nullptr; a.slot_sb = 0;
   a.x = static_cast<const f16*>(x); a.x_sb = x_sb; a.token = token;
   a.hidden_out = static_cast<f16*>(hidden_out); a.ho_sb = ho_sb;
   a.norm_w = static_cast<const f16*>(norm_w); a.eps = eps;
@@ -745,7 +769,51 @@ extern "C" int qf_rms_qkv_rope_append(const void* x, int64_t x_sb, const int64_t
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid((a.n_pairs + kNW - 1) / kNW), block(kNT);
   const size_t shm = 0;
-  QF_DISPATCH_B(B, rms_qkv_rope_append_kernel)
+  QF_DISPATCH_B(B, rms_qkv_rope_append_kernel, false)
+  return (int)hipGetLastError();
+}
+
+extern "C" int qf_rms_qkv_rope_append_paged(const void* x, int64_t x_sb, const int64_t* token,
+                                            void* hidden_out, int64_t ho_sb,
+                                            const void* norm_w, float eps,
+                                            const void* w_qkv, const void* bias,
+                                            const void* cos, const void* sin, int64_t cs_sb,
+                                            void* k_pool, int64_t kp_sp, int64_t kp_sh, int64_t kp_sn,
+                                            void* v_pool, int64_t vp_sp, int64_t vp_sh, int64_t vp_sn,
+                                            const int32_t* block_table, int64_t bt_sb,
+                                            int pages_per_row, int n_pages, int page_size,
+                                            const int64_t* slots, int64_t slot_sb,
+                                            void* q_out, int64_t qo_sb, int64_t qo_sh,
+                                            int B, int hidden, int QH, int KVH, int D,
+                                            void* stream) {
+  const int l2 = page_log2(page_size, pages_per_row, n_pages);
+  if (D != kHeadDim || l2 < 0) return QF_ERR_UNSUPPORTED;
+  if (B < 1 || B > kMaxB || hidden < 8 || hidden > kMaxNormK || hidden % 8) return QF_ERR_UNSUPPORTED;
+  if (!x || !norm_w || !w_qkv || !cos || !sin || !k_pool || !v_pool || !block_table || !slots ||
+      !q_out)
+    return QF_ERR_INVALID_ARG;
+  if (QH < 1 || KVH < 1 || bt_sb < pages_per_row) return QF_ERR_INVALID_ARG;
+  if (token != nullptr && hidden_out != nullptr && (!al16(hidden_out) || (ho_sb & 7)))
+    return QF_ERR_INVALID_ARG;
+  if (!al16(x) || !al16(norm_w) || !al16(w_qkv) || (x_sb & 7)) return QF_ERR_INVALID_ARG;
+  QkvArgs a;
+  a.x = static_cast<const f16*>(x); a.x_sb = x_sb; a.token = token;
+  a.hidden_out = static_cast<f16*>(hidden_out); a.ho_sb = ho_sb;
+  a.norm_w = static_cast<const f16*>(norm_w); a.eps = eps;
+  a.w = static_cast<const f16*>(w_qkv); a.bias = static_cast<const f16*>(bias);
+  a.cos = static_cast<const f16*>(cos); a.sin = static_cast<const f16*>(sin); a.cs_sb = cs_sb;
+  a.kc = static_cast<f16*>(k_pool); a.kc_sb = kp_sp; a.kc_sh = kp_sh; a.kc_sn = kp_sn;
+  a.vc = static_cast<f16*>(v_pool); a.vc_sb = vp_sp; a.vc_sh = vp_sh; a.vc_sn = vp_sn;
+  a.write_index = nullptr;
+  a.q_out = static_cast<f16*>(q_out); a.qo_sb = qo_sb; a.qo_sh = qo_sh;
+  a.K = hidden; a.QH = QH; a.KVH = KVH; a.cap = pages_per_row * page_size;
+  a.n_pairs = (QH + 2 * KVH) * (kHeadDim / 2);
+  a.table = block_table; a.t_sb = bt_sb; a.log2p = l2; a.n_pages = n_pages;
+  a.slots = slots; a.slot_sb = slot_sb;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid((a.n_pairs + kNW - 1) / kNW), block(kNT);
+  const size_t shm = 0;
+  QF_DISPATCH_B(B, rms_qkv_rope_append_kernel, true)
   return (int)hipGetLastError();
 }
 

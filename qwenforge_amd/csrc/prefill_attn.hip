@@ -29,6 +29,7 @@
 // the diagonal and tail tiles.
 #include "qf_common.h"
 #include "../../include/qf_attn.h"
+#include "../../include/qf_paged.h"
 
 namespace qf {
 
@@ -74,7 +75,26 @@ struct Args {
   const int* cu;
   int total;  // packed token count (bounds every row)
   int kv_packed;
+  // Paged caches: kc/vc are page pools (page strides kc_sb/vc_sb); slot s of
+  // row b lives in page table[b * t_sb + (s >> log2p)] at row s & (P - 1).
+  // ppr = pages per row.
+  const int32_t* table;
+  int64_t t_sb;
+  int log2p, n_pages, ppr;
 };
+
+// Element offset of slot `slot` of row b (kv head 0) in a cache: contiguous,
+// or through the block table (ok = false for a page outside the pool).
+__device__ __forceinline__ int64_t cache_row(const Args& a, int b, int64_t slot, int64_t sb,
+                                             int64_t sn, bool& ok) {
+  if (a.table == nullptr) {
+    ok = true;
+    return b * sb + slot * sn;
+  }
+  const int page = a.table[b * a.t_sb + (slot >> a.log2p)];
+  ok = page >= 0 && page < a.n_pages;
+  return (int64_t)page * sb + (slot & ((1 << a.log2p) - 1)) * sn;
+}
 
 // Token count and first packed token of row b, clamped to [0, total) and to
 // the longest row S, so any cu contents keep every access in bounds.
@@ -405,6 +425,14 @@ struct LdsCtx {
   const unsigned char* vnext;
   int64_t krem, vrem;
   int64_t k_sn, v_sn;
+  // Paged caches: tile kt_issue's rows start in the page of slot
+  // start + 64 * kt_issue; lane j of `pid` holds the physical page of
+  // logical page pwin + j of this row (`trow`), reloaded every 64 pages.
+  const unsigned char* kpool;  // pool + kv head offset (bytes)
+  const unsigned char* vpool;
+  const int32_t* trow;
+  int64_t k_sp, v_sp, start;   // page strides (bytes), first slot of the sequence
+  int pid, pwin, kt_issue, log2p, ppr, n_pages;
   int S, mt, qrow, n_ktiles, grp, lrow0, pch, w;
   int koff[2][2][2];  // [ch][j][kk] LDS byte offsets of the K operand reads
   int voff[2][4][2];  // [ch][d tile][h] LDS byte offsets of the V^T reads
@@ -424,9 +452,32 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const unsigned char*
                                            (int)(rem < 0x7fffffff ? rem : 0x7fffffff), 0x00020000);
 }
 
+// Physical pages of logical pages [win, win + 64) of the row into lane j,
+// clamped to the row's table and to the pool.
+__device__ __forceinline__ void load_pids(LdsCtx& c, int win) {
+  int j = win + (threadIdx.x & 63);
+  j = j < c.ppr ? j : c.ppr - 1;
+  const int p = c.trow[j];
+  c.pid = min(max(p, 0), c.n_pages - 1);
+  c.pwin = win;
+}
+
 // Async loads of the next tile (this wave's 16 rows of K and of V) into
-// (Kd, Vd); advances the issue cursor by one tile (scalar adds only).
+// (Kd, Vd); advances the issue cursor by one tile (scalar adds only).  Paged
+// caches: the tile's rows lie in one page (start and the page size are
+// multiples of 64), whose base comes from the page ids held in `pid`.
+template <bool kPaged>
 __device__ __forceinline__ void lds_issue(LdsCtx& c, unsigned char* Kd, unsigned char* Vd) {
+  if (kPaged) {
+    const int64_t slot0 = c.start + (int64_t)c.kt_issue * kBN;
+    const int lp = (int)(slot0 >> c.log2p);
+    if (lp - c.pwin >= 64) load_pids(c, lp);
+    const int page = __builtin_amdgcn_readlane(c.pid, lp - c.pwin);
+    const int64_t row = slot0 & ((1 << c.log2p) - 1);
+    c.knext = c.kpool + (int64_t)page * c.k_sp + row * c.k_sn * 2;
+    c.vnext = c.vpool + (int64_t)page * c.v_sp + row * c.v_sn * 2;
+    ++c.kt_issue;
+  }
   const __amdgpu_buffer_rsrc_t rk = tile_rsrc(c.knext, c.krem);
   const __amdgpu_buffer_rsrc_t rv = tile_rsrc(c.vnext, c.vrem);
 #pragma unroll
@@ -464,6 +515,7 @@ __device__ __forceinline__ float max16(const f32x4 (&sc)[4]) {
 
 // One tile: wait for its loads, refill the stage of tile kt-1 with tile kt+2,
 // then scores, online softmax and PV from (Ks, Vs).
+template <bool kPaged>
 __device__ __forceinline__ void lds_step(LdsCtx& c, int kt, const unsigned char* Ks,
                                          const unsigned char* Vs, unsigned char* Kn,
                                          unsigned char* Vn) {
@@ -487,7 +539,7 @@ __device__ __forceinline__ void lds_step(LdsCtx& c, int kt, const unsigned char*
       for (int kk = 0; kk < 2; ++kk)
         ka[ch][j][kk] = *reinterpret_cast<const f16x8*>(Ks + c.koff[ch][j][kk]);
   // Refill after the K operands are in registers (the V^T reads come later).
-  if (kt + 2 < c.n_ktiles) lds_issue(c, Kn, Vn);  // tile kt + 2
+  if (kt + 2 < c.n_ktiles) lds_issue<kPaged>(c, Kn, Vn);  // tile kt + 2
   f32x4 sc[4];
 #pragma unroll
   for (int ch = 0; ch < 2; ++ch)
@@ -542,7 +594,7 @@ __device__ __forceinline__ void lds_step(LdsCtx& c, int kt, const unsigned char*
     }
 }
 
-template <bool kRopeQ>
+template <bool kRopeQ, bool kPaged>
 __global__ __launch_bounds__(kWaves * 64) void prefill_lds_kernel(Args a) {
   // Three stages, each its own K and V array so that loads into one stage are
   // visibly disjoint from reads of another (no conservative waits).
@@ -627,8 +679,21 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_lds_kernel(Args a) {
   c.vnext = reinterpret_cast<const unsigned char*>(c.vb + (int64_t)kt0 * kBN * c.v_sn);
   c.krem = (int64_t)(S - kt0 * kBN) * c.k_sn * 2;
   c.vrem = (int64_t)(S - kt0 * kBN) * c.v_sn * 2;
-  lds_issue(c, k0, v0);                                // tile kt0
-  if (kt0 + 1 < c.n_ktiles) lds_issue(c, k1, v1);      // tile kt0 + 1
+  if (kPaged) {
+    c.kpool = reinterpret_cast<const unsigned char*>(a.k + hk * a.k_sh);
+    c.vpool = reinterpret_cast<const unsigned char*>(a.v + hk * a.v_sh);
+    c.trow = a.table + b * a.t_sb;
+    c.k_sp = a.k_sb * 2;
+    c.v_sp = a.v_sb * 2;
+    c.start = a.start_pos;
+    c.log2p = a.log2p;
+    c.ppr = a.ppr;
+    c.n_pages = a.n_pages;
+    c.kt_issue = kt0;
+    load_pids(c, (int)((a.start_pos + (int64_t)kt0 * kBN) >> a.log2p));
+  }
+  lds_issue<kPaged>(c, k0, v0);                            // tile kt0
+  if (kt0 + 1 < c.n_ktiles) lds_issue<kPaged>(c, k1, v1);  // tile kt0 + 1
   if (kRopeQ) rope_pair(c.qf[0], c.qf[1], qcs[0], qcs[1], qcs[2], qcs[3]);
 
 #pragma unroll
@@ -656,9 +721,9 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_lds_kernel(Args a) {
   for (int t = 0; t < 4; ++t) c.o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   for (int kt = kt0; kt < c.n_ktiles; kt += kStages) {
-    lds_step(c, kt, k0, v0, k2, v2);
-    if (kt + 1 < c.n_ktiles) lds_step(c, kt + 1, k1, v1, k0, v0);
-    if (kt + 2 < c.n_ktiles) lds_step(c, kt + 2, k2, v2, k1, v1);
+    lds_step<kPaged>(c, kt, k0, v0, k2, v2);
+    if (kt + 1 < c.n_ktiles) lds_step<kPaged>(c, kt + 1, k1, v1, k0, v0);
+    if (kt + 2 < c.n_ktiles) lds_step<kPaged>(c, kt + 2, k2, v2, k1, v1);
   }
 
   const float l_run = c.l4[0];
@@ -774,6 +839,7 @@ __global__ __launch_bounds__(256) void rope_kv_prefill_kernel(Args a) {
   if (tok >= S || sub >= 12) return;
   const int64_t slot = a.start_pos + tok;
   const int64_t t = tok0 + tok;  // packed token index (== tok for equal-length rows)
+  bool ok;
   if (sub < 4) {
     const f16* src = a.k + b * a.k_sb + h * a.k_sh + t * a.k_sn + 8 * sub;
     f16x8 lo = load16(src), hi = load16(src + 32);
@@ -782,13 +848,16 @@ __global__ __launch_bounds__(256) void rope_kv_prefill_kernel(Args a) {
       rope_pair(lo, hi, load16(a.cos + co), load16(a.sin + co), load16(a.cos + co + 32),
                 load16(a.sin + co + 32));
     }
-    f16* dst = a.kc + b * a.kc_sb + h * a.kc_sh + slot * a.kc_sn + 8 * sub;
-    store16(dst, lo);
-    store16(dst + 32, hi);
+    f16* dst = a.kc + cache_row(a, b, slot, a.kc_sb, a.kc_sn, ok) + h * a.kc_sh + 8 * sub;
+    if (ok) {
+      store16(dst, lo);
+      store16(dst + 32, hi);
+    }
   } else {
     const int c = sub - 4;
-    store16(a.vc + b * a.vc_sb + h * a.vc_sh + slot * a.vc_sn + 8 * c,
-            load16(a.v + b * a.v_sb + h * a.v_sh + t * a.v_sn + 8 * c));
+    const f16x8 val = load16(a.v + b * a.v_sb + h * a.v_sh + t * a.v_sn + 8 * c);
+    f16* dst = a.vc + cache_row(a, b, slot, a.vc_sb, a.vc_sn, ok) + h * a.vc_sh + 8 * c;
+    if (ok) store16(dst, val);
   }
 }
 
@@ -867,15 +936,19 @@ static int prefill_launch(Args a, bool rope, bool append, hipStream_t st) {
     hipLaunchKernelGGL((prefill_kernel<true, false>), grid, block, 0, st, a);
     return (int)hipGetLastError();
   }
+  const bool paged = a.table != nullptr;
   if (append) {
     // Pre-pass: rotated K (or K as is) and V into the cache; then stream the
-    // finished rows back from the cache.
+    // finished rows back from the cache (paged: the kernel finds each tile's
+    // page from start_pos and the block table).
     hipLaunchKernelGGL(rope_kv_prefill_kernel, dim3((S + 15) / 16, B * KVH), dim3(256), 0, st, a);
-    a.k = a.kc + a.start_pos * a.kc_sn;
+    a.k = a.kc + (paged ? 0 : a.start_pos * a.kc_sn);
     a.k_sb = a.kc_sb; a.k_sh = a.kc_sh; a.k_sn = a.kc_sn;
-    a.v = a.vc + a.start_pos * a.vc_sn;
+    a.v = a.vc + (paged ? 0 : a.start_pos * a.vc_sn);
     a.v_sb = a.vc_sb; a.v_sh = a.vc_sh; a.v_sn = a.vc_sn;
     a.kv_packed = 0;
+  } else if (paged) {
+    return QF_ERR_INVALID_ARG;  // paged prefill always appends
   }
   int n_items = grid.x, n_merge = 0;
   if (a.split_tiles > 0) {
@@ -883,8 +956,13 @@ static int prefill_launch(Args a, bool rope, bool append, hipStream_t st) {
     split_plan(S, st_, mp_, n_items, n_merge);
   }
   const dim3 lgrid(n_items, B * QH);
-  if (rope) hipLaunchKernelGGL((prefill_lds_kernel<true>), lgrid, block, 0, st, a);
-  else hipLaunchKernelGGL((prefill_lds_kernel<false>), lgrid, block, 0, st, a);
+  if (paged) {
+    if (rope) hipLaunchKernelGGL((prefill_lds_kernel<true, true>), lgrid, block, 0, st, a);
+    else hipLaunchKernelGGL((prefill_lds_kernel<false, true>), lgrid, block, 0, st, a);
+  } else {
+    if (rope) hipLaunchKernelGGL((prefill_lds_kernel<true, false>), lgrid, block, 0, st, a);
+    else hipLaunchKernelGGL((prefill_lds_kernel<false, false>), lgrid, block, 0, st, a);
+  }
   if (n_merge > 0)
     hipLaunchKernelGGL(prefill_merge_kernel, dim3(n_merge, B * QH), dim3(256), 0, st, a);
   return (int)hipGetLastError();
@@ -930,6 +1008,11 @@ static int fill_common(Args& a, const void* q, const void* k, const void* v, con
   a.cu = nullptr;
   a.total = 0;
   a.kv_packed = 1;
+  a.table = nullptr;
+  a.t_sb = 0;
+  a.log2p = 0;
+  a.n_pages = 0;
+  a.ppr = 0;
   return QF_OK;
 }
 
@@ -997,5 +1080,46 @@ extern "C" int qf_prefill_varlen(const void* q, int64_t q_sh, int64_t q_sn,
   a.o_sb = 0; a.o_sh = o_sh; a.o_sn = o_sn;
   a.cu = cu_seqlens;
   a.total = total;
+  return prefill_launch(a, rope, append, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int qf_prefill_varlen_paged(const void* q, int64_t q_sh, int64_t q_sn,
+                                       const void* k, int64_t k_sh, int64_t k_sn,
+                                       const void* v, int64_t v_sh, int64_t v_sn,
+                                       const int32_t* cu_seqlens, int total, int max_seqlen,
+                                       const void* cos, const void* sin, int64_t cs_sn,
+                                       void* k_pool, int64_t kp_sp, int64_t kp_sh, int64_t kp_sn,
+                                       void* v_pool, int64_t vp_sp, int64_t vp_sh, int64_t vp_sn,
+                                       const int32_t* block_table, int64_t bt_sb,
+                                       int pages_per_row, int n_pages, int page_size,
+                                       int64_t start_pos,
+                                       void* out, int64_t o_sh, int64_t o_sn,
+                                       int B, int QH, int KVH, int D, float scale, void* stream) {
+  using namespace qf::prefill;
+  const int l2 = page_log2(page_size, pages_per_row, n_pages);
+  if (l2 < 0) return QF_ERR_UNSUPPORTED;
+  if (!cu_seqlens || total < 1 || !block_table || !k_pool || !v_pool) return QF_ERR_INVALID_ARG;
+  if (bt_sb < pages_per_row || start_pos % kBN != 0) return QF_ERR_INVALID_ARG;
+  Args a;
+  bool rope, append;
+  const int rc = fill_common(a, q, k, v, cos, sin, k_pool, kp_sp, kp_sh, kp_sn, v_pool, vp_sp,
+                             vp_sh, vp_sn, start_pos, pages_per_row * page_size, out, B, QH, KVH,
+                             max_seqlen, D, scale, rope, append);
+  if (rc != QF_OK) return rc;
+  if ((q_sh | q_sn | k_sh | k_sn | v_sh | v_sn) & 7) return QF_ERR_INVALID_ARG;
+  if ((o_sh | o_sn) & 3) return QF_ERR_INVALID_ARG;
+  if (rope && (cs_sn & 7)) return QF_ERR_INVALID_ARG;
+  a.q_sb = 0; a.q_sh = q_sh; a.q_sn = q_sn;
+  a.k_sb = 0; a.k_sh = k_sh; a.k_sn = k_sn;
+  a.v_sb = 0; a.v_sh = v_sh; a.v_sn = v_sn;
+  a.cs_sb = 0; a.cs_sn = cs_sn;
+  a.o_sb = 0; a.o_sh = o_sh; a.o_sn = o_sn;
+  a.cu = cu_seqlens;
+  a.total = total;
+  a.table = block_table;
+  a.t_sb = bt_sb;
+  a.log2p = l2;
+  a.n_pages = n_pages;
+  a.ppr = pages_per_row;
   return prefill_launch(a, rope, append, static_cast<hipStream_t>(stream));
 }

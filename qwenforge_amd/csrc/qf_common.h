@@ -82,4 +82,17 @@ __device__ __forceinline__ float col_sum(float x) {
   return x;
 }
 
+// Paged KV caches (host side): page_size must be a power of two in
+// [64, 4096] (a 32-key decode tile and a 64-key prefill tile then never
+// straddle a page), with at least one page per row and a non-empty pool.
+// Returns log2(page_size), or -1 when the geometry is unsupported.
+inline int page_log2(int page_size, int pages_per_row, int n_pages) {
+  if (page_size < 64 || page_size > 4096 || (page_size & (page_size - 1)) != 0) return -1;
+  if (pages_per_row < 1 || n_pages < 1) return -1;
+  if ((int64_t)pages_per_row * page_size > 0x7fffffff) return -1;
+  int l = 0;
+  while ((1 << l) < page_size) ++l;
+  return l;
+}
+
 }  // namespace qf

@@ -116,17 +116,24 @@ def ticket_size(batch: int, kv_heads: int, splits: int) -> int:
 
 def _decode_args(grouped, key_cache, value_cache, attn_bias, flash, kv_last):
     """Validate the decode operands; returns the parsed pieces."""
-    acc, m, l, out = flash[:4]
-    ticket = flash[4] if len(flash) > 4 else None
     _require_cuda_fp16("grouped", grouped, 4)
     _require_cuda_fp16("key_cache", key_cache, 4)
     _require_cuda_fp16("value_cache", value_cache, 4)
-    _require_cuda_fp16("out", out, 4)
-    b, kvh, g, d = grouped.shape
-    cap = key_cache.shape[2]
+    b, kvh = grouped.shape[:2]
     if key_cache.shape[:2] != (b, kvh) or value_cache.shape != key_cache.shape:
         raise ValueError(f"cache shape {tuple(key_cache.shape)} / {tuple(value_cache.shape)} "
                          f"does not match grouped {tuple(grouped.shape)}")
+    return _scratch_args(grouped, key_cache.shape[2], attn_bias, flash, kv_last)
+
+
+def _scratch_args(grouped, cap, attn_bias, flash, kv_last):
+    """Validate the query, bias, bound and scratch operands of a decode call
+    over ``cap`` slots per row; returns the parsed pieces."""
+    acc, m, l, out = flash[:4]
+    ticket = flash[4] if len(flash) > 4 else None
+    _require_cuda_fp16("grouped", grouped, 4)
+    _require_cuda_fp16("out", out, 4)
+    b, kvh, g, d = grouped.shape
     splits = acc.shape[2]
     if acc.shape != (b, kvh, splits, g, d) or m.shape != (b, kvh, splits, g) or l.shape != m.shape:
         raise ValueError("flash scratch shapes do not match (B, KVH, S, G, D) / (B, KVH, S, G)")

@@ -41,7 +41,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_version_and_error_strings():
     lib = _lib.load()
-    assert lib.qf_abi_version() == 101
+    assert lib.qf_abi_version() == 102
     assert lib.qf_error_string(0) == b"success"
     assert b"invalid" in lib.qf_error_string(-1)
     assert b"unsupported" in lib.qf_error_string(-2)
@@ -157,3 +157,54 @@ def test_prefill_varlen_rejects_bad_arguments():
     assert call(total=0) == -1
     assert call(cos=16, sin=16) == -2               # RoPE needs the caches
     assert call(kc=16, vc=16, cap=4) == -1          # max_seqlen exceeds capacity
+
+
+def test_paged_entry_points_reject_bad_arguments():
+    lib = _lib.load()
+
+    def decode(page=64, ppr=4, n_pages=8, table=16, bt_sb=4, kp_sp=2 * 64 * 64, out=16):
+        return lib.qf_decode_attn_paged(16, 0, 0, 0, 16, kp_sp, 64 * 64, 64, 16, 2 * 64 * 64,
+                                        64 * 64, 64, table, bt_sb, ppr, n_pages, page,
+                                        None, 0, None, 0, 16, 16, 16, 1, None, out, 0, 0, 0,
+                                        1, 2, 7, 64, 0.125, None)
+
+    assert decode(page=32) == -2          # below the 64-slot minimum
+    assert decode(page=96) == -2          # not a power of two
+    assert decode(page=8192) == -2        # above the maximum
+    assert decode(ppr=0) == -2
+    assert decode(n_pages=0) == -2
+    assert decode(table=None) == -1
+    assert decode(bt_sb=2) == -1          # table rows overlap
+    assert decode(kp_sp=2 * 64 * 64 + 4) == -1  # page stride breaks 16-byte rows
+    assert decode(out=None) == -1
+
+    def append(page=64, slots=16, table=16):
+        return lib.qf_rope_append_paged(16, 0, 0, 16, 0, 0, 16, 0, 0, 16, 16, 0,
+                                        16, 8192, 4096, 64, 16, 8192, 4096, 64,
+                                        table, 4, 4, 8, page, slots, 1, 16, 0, 0,
+                                        1, 14, 2, 64, None)
+
+    assert append(page=48) == -2
+    assert append(slots=None) == -1
+    assert append(table=None) == -1
+
+    def prefill(start=0, max_seqlen=8, ppr=4, table=16):
+        return lib.qf_prefill_varlen_paged(16, 64, 896, 16, 64, 128, 16, 64, 128, 16, 8,
+                                           max_seqlen, None, None, 0,
+                                           16, 8192, 4096, 64, 16, 8192, 4096, 64,
+                                           table, 4, ppr, 8, 64, start,
+                                           16, 64, 896, 2, 14, 2, 64, 0.125, None)
+
+    assert prefill(start=32) == -1        # start must be tile-aligned
+    assert prefill(table=None) == -1
+    assert prefill(start=256, max_seqlen=8) == -1  # past the row's 256 slots
+
+    def qkv(page=64, slots=16, B=1):
+        return lib.qf_rms_qkv_rope_append_paged(16, 896, None, None, 0, 16, 1e-6, 16, None,
+                                                16, 16, 64, 16, 8192, 4096, 64,
+                                                16, 8192, 4096, 64, 16, 4, 4, 8, page,
+                                                slots, 1, 16, 896, 64, B, 896, 14, 2, 64, None)
+
+    assert qkv(page=100) == -2
+    assert qkv(B=5) == -2
+    assert qkv(slots=None) == -1

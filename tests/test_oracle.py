@@ -275,6 +275,56 @@ def test_append_prefill_brute_force():
             assert float(gkc[:, :, s].abs().sum()) == 0.0
 
 
+def test_paged_identity_table_is_a_reshape():
+    """Closed form: with table[b, j] = b * ppr + j the pool is the dense cache
+    cut into pages, (B, KVH, ppr, P, D) -> (B * ppr, KVH, P, D)."""
+    gen = torch.Generator().manual_seed(21)
+    b, kvh, ppr, page, d = 3, 2, 4, 64, 64
+    dense = _rand(gen, b, kvh, ppr * page, d)
+    table = torch.arange(b * ppr, dtype=torch.int32).view(b, ppr)
+    full = [ppr * page] * b
+    pool = oracle.dense_to_pages(dense, table, full, b * ppr, page)
+    closed = dense.view(b, kvh, ppr, page, d).permute(0, 2, 1, 3, 4).reshape(b * ppr, kvh, page, d)
+    assert torch.equal(pool, closed)
+    assert torch.equal(oracle.pages_to_dense(closed, table, full, ppr * page), dense)
+    assert oracle.paged_location(table, 1, 130, page) == (1 * ppr + 2, 2)
+
+
+def test_paged_gather_scatter_inverse_on_random_tables():
+    gen = torch.Generator().manual_seed(22)
+    b, kvh, ppr, page, d, n_pages = 3, 2, 3, 64, 64, 11
+    lengths = [150, 64, 1]
+    perm = torch.randperm(n_pages, generator=gen).to(torch.int32)
+    table = perm[: b * ppr].view(b, ppr)
+    dense = _rand(gen, b, kvh, ppr * page, d)
+    for r, n in enumerate(lengths):
+        dense[r, :, n:] = 0
+    pool = oracle.dense_to_pages(dense, table, lengths, n_pages, page)
+    assert torch.equal(oracle.pages_to_dense(pool, table, lengths, ppr * page), dense)
+    # Pages no row maps stay zero.
+    unused = perm[b * ppr:].tolist()
+    assert float(pool[unused].abs().sum()) == 0.0
+
+
+def test_append_rows_brute_force():
+    gen = torch.Generator().manual_seed(23)
+    kc = _rand(gen, 3, 2, 9, 64)
+    vc = _rand(gen, 3, 2, 9, 64)
+    k = _rand(gen, 3, 2, 1, 64)
+    v = _rand(gen, 3, 2, 1, 64)
+    slots = [4, 0, 9]  # row 2 is out of range: nothing written
+    ekc, evc = kc.clone(), vc.clone()
+    for r, s in enumerate(slots[:2]):
+        ekc[r, :, s] = k[r, :, 0]
+        evc[r, :, s] = v[r, :, 0]
+    gkc, gvc = oracle.append_rows(kc.clone(), vc.clone(), k, v, torch.tensor(slots))
+    assert torch.equal(gkc, ekc) and torch.equal(gvc, evc)
+    # One shared slot reduces to the reference's index_copy_ append.
+    skc, svc = oracle.append_rows(kc.clone(), vc.clone(), k, v, torch.tensor([5, 5, 5]))
+    rkc, rvc = oracle.append_decode(kc.clone(), vc.clone(), k, v, torch.tensor([5]))
+    assert torch.equal(skc, rkc) and torch.equal(svc, rvc)
+
+
 def test_capacity_rule_brute_force():
     for p in range(1, 140, 7):
         for n in range(0, 70, 9):
