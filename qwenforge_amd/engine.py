@@ -111,6 +111,13 @@ class DecodeEngine:
         GEMM over all tokens and one varlen launch does RoPE, the cache append
         (slots [0, len_b) of row b) and the causal attention of every row.
         """
+        return self._prefill_packed(
+            prompts, lambda i, q, k, v, cu, n, cos, sin: ops.prefill_varlen(
+                q, k, v, cu, n, cos, sin, caches[i][0], caches[i][1], 0))
+
+    def _prefill_packed(self, prompts, attend):
+        """Packed ragged prefill body; ``attend(layer, q, k, v, cu, max_len, cos,
+        sin)`` runs the varlen RoPE + append + attention launch of one layer."""
         cfg = self.cfg
         dev = self.device
         lengths = [int(p.numel()) for p in prompts]
@@ -124,14 +131,14 @@ class DecodeEngine:
         cos, sin = cos_sin(pos, self.inv_freq)                 # (T, D): each row's own positions
         qw, kvw = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
         hidden = F.embedding(ids, self.w["embed"])
-        for layer, (kc, vc) in zip(self.w["layers"], caches):
+        for i, layer in enumerate(self.w["layers"]):
             residual = hidden
             proj = F.linear(self._rms(hidden, layer["input_norm"]), layer["qkv_weight"],
                             layer["qkv_bias"])
             q = proj[:, :qw].view(total, cfg.heads, cfg.head_dim)
             k = proj[:, qw:qw + kvw].view(total, cfg.kv_heads, cfg.head_dim)
             v = proj[:, qw + kvw:].view(total, cfg.kv_heads, cfg.head_dim)
-            att = ops.prefill_varlen(q, k, v, cu, max(lengths), cos, sin, kc, vc, 0)
+            att = attend(i, q, k, v, cu, max(lengths), cos, sin)
             hidden = residual + F.linear(att.reshape(total, cfg.hidden), layer["o_weight"])
             residual = hidden
             hidden = residual + self._mlp(self._rms(hidden, layer["post_norm"]), layer)
