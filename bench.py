@@ -9,10 +9,11 @@ Replicated cache sets (> 256 MB, the MI355X Infinity Cache) are cycled so each
 step reads its K/V from HBM.  ``value`` = algorithmic bytes (valid K/V + q +
 out) per step / step time, in GB/s.
 
-Extra keys report the long-context decode (config 3), the fused
-RoPE+append prefill (config 4) and, when available, the end-to-end
-Qwen2.5-0.5B-shaped decode step (config 5).  ``cpu_baseline`` times the CPU
-oracle on a bounded sample of the same workload.
+Extra keys report the long-context decode (config 3), the bandwidth-bound
+decode shapes (dense and paged caches), the fused RoPE+append prefill
+(config 4) and the end-to-end Qwen2.5-0.5B-shaped decode step (config 5:
+dense, ragged, paged and continuous batching).  ``cpu_baseline`` times the
+CPU oracle on a bounded sample of the same workload.
 """
 
 from __future__ import annotations
@@ -196,6 +197,102 @@ def bench_bandwidth_decode(steps, warmup, dev, batch, length):
     nbytes = base.valid_bytes
     return dict(batch=batch, length=length, splits=splits, fused=len(flash) > 4,
                 us_full=ms_full * 1e3, us_split=ms_split * 1e3, bytes=nbytes)
+
+
+def _to_pages(dense, page, perm):
+    """(B, KVH, cap, D) cache -> (B*cap/page, KVH, page, D) pool whose page
+    b*ppr + j holds logical page j of row b at physical index perm[b*ppr + j]."""
+    b, kvh, cap, d = dense.shape
+    ppr = cap // page
+    pages = dense.view(b, kvh, ppr, page, d).permute(0, 2, 1, 3, 4).reshape(b * ppr, kvh, page, d)
+    pool = dense.new_empty(pages.shape)
+    pool[perm] = pages
+    return pool
+
+
+def bench_paged_decode(steps, warmup, dev, batch, length, page=64):
+    """The bandwidth-regime decode over a paged cache: the same K/V as
+    ``bench_bandwidth_decode`` cut into 64-slot pages placed by a random
+    permutation, read through the block table."""
+    import torch
+
+    from qwenforge_amd import ops, paged, workloads
+
+    base = workloads.decode_uniform(batch, length, seed=1)
+    per = base.key_cache.numel() * 2 * 2
+    reps = max(2, -(-2 * MALL_BYTES // per))
+    q = base.grouped.to(dev)
+    ppr = length // page
+    perm = torch.randperm(batch * ppr, generator=torch.Generator().manual_seed(0)).to(dev)
+    table = perm.view(batch, ppr).to(torch.int32)
+    k0, v0 = base.key_cache.to(dev), base.value_cache.to(dev)
+    kp = [_to_pages(k0, page, perm)] + [None] * (reps - 1)
+    vp = [_to_pages(v0, page, perm)] + [None] * (reps - 1)
+    for r in range(1, reps):
+        kp[r], vp[r] = kp[0].clone(), vp[0].clone()
+    del k0, v0
+    splits = ops.choose_splits(batch, 2, length)
+    flash = ops.make_flash_scratch(batch, 2, 7, length, dev, splits=splits)
+
+    def full():
+        for r in range(reps):
+            paged.flash_decode_attention_paged(q, kp[r], vp[r], table, None, flash)
+
+    def split_only():
+        for r in range(reps):
+            paged.flash_decode_split_paged(q, kp[r], vp[r], table, None, flash[:4])
+
+    ms_full = _time_graphs([GraphStep(full)], max(1, steps // 4), max(1, warmup // 4)) / reps
+    ms_split = _time_graphs([GraphStep(split_only)], max(1, steps // 4), max(1, warmup // 4)) / reps
+    return dict(batch=batch, length=length, splits=splits, page=page,
+                us_full=ms_full * 1e3, us_split=ms_split * 1e3, bytes=base.valid_bytes)
+
+
+def bench_paged_e2e(dev, new_tokens=128):
+    """Config-5 model over a paged cache: the ragged batch of ``bench_e2e``
+    through ``generate_paged`` (each row holds only its own pages, no holes),
+    and continuous batching of 16 requests through 4 rows (``serve``)."""
+    import torch
+
+    from qwenforge_amd.model import Qwen2Config, init_weights
+    from qwenforge_amd.paged_engine import PagedDecodeEngine
+
+    cfg = Qwen2Config()
+    eng = PagedDecodeEngine(cfg, init_weights(cfg, dev, seed=0), dev)
+    lengths = (512, 700, 896, 1024)
+    gen = torch.Generator().manual_seed(7)
+    prompts = [torch.randint(0, cfg.vocab, (n,), generator=gen).to(dev) for n in lengths]
+    eng.generate_paged(prompts, 8)
+    timing = {}
+    eng.generate_paged(prompts, new_tokens, timing=timing)
+    steps = new_tokens - 1
+    out = {"ragged_bs4": {
+        "lengths": list(lengths),
+        "decode_tok_s": round(len(lengths) * steps / (timing["decode_ms"] * 1e-3), 1),
+        "ms_per_step": round(timing["decode_ms"] / steps, 4),
+        "prefill_ms": round(timing["prefill_ms"], 3),
+        "pages": timing["pages"],
+    }}
+    gen = torch.Generator().manual_seed(8)
+    n_req = 16
+    req_len = torch.randint(128, 1025, (n_req,), generator=gen).tolist()
+    req_new = torch.randint(16, 129, (n_req,), generator=gen).tolist()
+    reqs = [torch.randint(0, cfg.vocab, (n,), generator=gen).to(dev) for n in req_len]
+    eng.serve(reqs[:4], 4, max_batch=4)
+    torch.cuda.synchronize(dev)
+    stats = {}
+    t0 = time.perf_counter()
+    res = eng.serve(reqs, req_new, max_batch=4, stats=stats)
+    torch.cuda.synchronize(dev)
+    wall = time.perf_counter() - t0
+    n_tok = sum(int(x.numel()) for x in res)
+    out["serve"] = {
+        "requests": n_req, "max_batch": 4, "tokens": n_tok, "replays": stats["replays"],
+        "tok_s": round(n_tok / wall, 1), "wall_ms": round(wall * 1e3, 1),
+        "what": "16 requests (prompt 128-1024, 16-128 new tokens) through 4 rows, per-request "
+                "prefill on admission, wall clock including prefills and host scheduling",
+    }
+    return out
 
 
 def hbm_copy_ceiling(dev, mib=512, reps=20):
@@ -440,6 +537,20 @@ def main():
                 "merge": "fused single launch" if x["fused"] else "split + combine launches",
             }
         line["bandwidth_decode"] = bw
+        pg = {}
+        for b, L in ((16, 32768), (64, 4096)):
+            x = bench_paged_decode(args.steps, args.warmup, dev, b, L)
+            gbs_full = x["bytes"] / (x["us_full"] * 1e-6) / 1e9
+            dense = bw[f"B{b}_L{L}"]
+            pg[f"B{b}_L{L}"] = {
+                "page": x["page"],
+                "us_per_layer": round(x["us_full"], 3),
+                "GBps": round(gbs_full, 1),
+                "hbm_frac": round(gbs_full / HBM_PEAK_GBS, 4),
+                "split_kernel_us": round(x["us_split"], 3),
+                "vs_dense_cache": round(dense["us_per_layer"] / x["us_full"], 3),
+            }
+        line["paged_decode"] = pg
         copy_gbs = hbm_copy_ceiling(dev)
         line["hbm_copy_ceiling"] = {"GBps": round(copy_gbs, 1),
                                     "frac_of_peak": round(copy_gbs / HBM_PEAK_GBS, 4),
@@ -461,6 +572,7 @@ def main():
             "prefill_ms_bs4": e2e[4]["prefill_ms"],
             "weight_stream_GBps_bs1": e2e[1]["weight_GBps"],
             "ragged_bs4": e2e["ragged"],
+            "paged": bench_paged_e2e(dev),
             "workload": "24 layers, hidden 896, 14/2 heads, vocab 151936, random-init fp16 "
                         "(std 0.02), 1024-token random prefix, 128 greedy tokens; "
                         "tok/s = B*127 / graph-replay decode time",
