@@ -116,13 +116,15 @@ int qf_prefill_varlen_paged(const void* q, int64_t q_sh, int64_t q_sn,
 /*
  * The fused decode-step QKV projection (qf_rms_qkv_rope_append in qf_step.h:
  * rms_norm + QKV linear + RoPE + append, SE:917-932) appending into paged
- * caches at a per-row slot slots[b * slot_sb] read on the device.
+ * caches at a per-row slot slots[b * slot_sb] read on the device.  RoPE
+ * from cos/sin tables or from pos + inv_freq, as there.
  */
 int qf_rms_qkv_rope_append_paged(const void* x, int64_t x_sb, const int64_t* token,
                                  void* hidden_out, int64_t ho_sb,
                                  const void* norm_w, float eps,
                                  const void* w_qkv, const void* bias,
                                  const void* cos, const void* sin, int64_t cs_sb,
+                                 const int64_t* pos, const float* inv_freq,
                                  void* k_pool, int64_t kp_sp, int64_t kp_sh, int64_t kp_sn,
                                  void* v_pool, int64_t vp_sp, int64_t vp_sh, int64_t vp_sn,
                                  const int32_t* block_table, int64_t bt_sb, int pages_per_row,

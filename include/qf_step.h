@@ -35,7 +35,11 @@ extern "C" {
  * embedding table, :896) and, if `hidden_out` is non-null, the gathered rows
  * are also written to hidden_out (row stride ho_sb) as the residual stream.
  * w_qkv: ((QH + 2*KVH) * 64, hidden); bias: (QH + 2*KVH) * 64 or null.
- * cos/sin: (B, 64) fp16 tables, row stride cs_sb.  Rotated q goes to q_out
+ * RoPE angles come from either cos/sin: (B, 64) fp16 tables, row stride
+ * cs_sb (pos and inv_freq NULL), or pos: (B,) int64 positions plus inv_freq:
+ * (32,) fp32 (cos and sin NULL), in which case the table entries
+ * fp16(cos(float(pos[b]) * inv_freq[i])) (and sin) are formed in the kernel,
+ * bit-identical to the torch-built table of :910-915.  Rotated q goes to q_out
  * (B, QH, 64) with strides (qo_sb, qo_sh); rotated k and raw v go to slot
  * write_index[0] of the (B, KVH, cap, 64) caches (skipped when the slot is
  * outside [0, cap)).  Rounding: fp16(acc + bias) per projection output, then
@@ -46,6 +50,7 @@ int qf_rms_qkv_rope_append(const void* x, int64_t x_sb, const int64_t* token,
                            const void* norm_w, float eps,
                            const void* w_qkv, const void* bias,
                            const void* cos, const void* sin, int64_t cs_sb,
+                           const int64_t* pos, const float* inv_freq,
                            void* k_cache, int64_t kc_sb, int64_t kc_sh, int64_t kc_sn,
                            void* v_cache, int64_t vc_sb, int64_t vc_sh, int64_t vc_sn,
                            const int64_t* write_index,

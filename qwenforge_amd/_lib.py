@@ -103,6 +103,7 @@ SIGNATURES = {
         _vp, _f32,                      # norm_w, eps
         _vp, _vp,                       # w_qkv, bias
         _vp, _vp, _i64,                 # cos, sin, cs_sb
+        _vp, _vp,                       # pos, inv_freq
         _vp, _i64, _i64, _i64,          # k_cache
         _vp, _i64, _i64, _i64,          # v_cache
         _vp,                            # write_index
@@ -199,6 +200,7 @@ SIGNATURES = {
         _vp, _f32,                      # norm_w, eps
         _vp, _vp,                       # w_qkv, bias
         _vp, _vp, _i64,                 # cos, sin, cs_sb
+        _vp, _vp,                       # pos, inv_freq
         _vp, _i64, _i64, _i64,          # k_pool
         _vp, _i64, _i64, _i64,          # v_pool
         _vp, _i64, _i32, _i32, _i32,    # block_table, bt_sb, pages_per_row, n_pages, page_size

@@ -42,7 +42,10 @@ constexpr int kD = 64;
 constexpr int kTile = 32;       // keys per wave iteration
 constexpr int kVtStride = 36;   // LDS row stride (halves) of a transposed V tile
 constexpr int kMaxG = 16;
-constexpr int kGroup = 16;      // splits per first-level merge group
+#ifndef QF_DECODE_GROUP
+#define QF_DECODE_GROUP 16
+#endif
+constexpr int kGroup = QF_DECODE_GROUP;  // splits per first-level merge group
 
 enum Mode { kDirect = 0, kPartial = 1, kFused = 2 };
 
@@ -513,11 +516,16 @@ using namespace qf;
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Waves per workgroup (measured on MI355X): eight for up to two workgroups
-// per CU, sixteen when only a handful of CUs get work, four for large grids.
+// Waves per workgroup (measured on MI355X): sixteen when one workgroup per
+// kv head streams everything, eight up to two workgroups per CU (also for
+// small grids: at B=1 with 8 splits, 8 waves beat 16 by 0.7 us per call), four
+// for large grids.
 static int pick_waves(int splits, int B, int KVH) {
+#ifdef QF_DECODE_FORCE_NW
+  return QF_DECODE_FORCE_NW;
+#endif
   const int64_t wgs = (int64_t)splits * B * KVH;
-  if (wgs <= 16) return 16;
+  if (wgs <= 2) return 16;
   if (wgs <= 512) return 8;
   return 4;
 }

@@ -215,6 +215,12 @@ struct QkvArgs {
   const f16* cos;
   const f16* sin;
   int64_t cs_sb;
+  // Positions mode (cos == nullptr): row b's angle for frequency i is
+  // float(pos[b]) * inv_freq[i], and cos/sin are evaluated here in fp32 and
+  // rounded to fp16 -- bit-identical to the torch table (SE:910-915) that
+  // table mode reads.
+  const int64_t* pos;
+  const float* inv_freq;
   f16* kc;
   int64_t kc_sb, kc_sh, kc_sn;
   f16* vc;
@@ -234,7 +240,7 @@ struct QkvArgs {
 };
 
 // One wave per (head, d) rotate-half pair: rows head*64 + d and head*64 + d + 32.
-template <int NB, bool kPaged>
+template <int NB, bool kPaged, bool kPos>
 __global__ __launch_bounds__(kNT) void rms_qkv_rope_append_kernel(QkvArgs a) {
   constexpr int NS = kMaxNormK / 8 / 64;  // 2
   __shared__ __attribute__((aligned(16))) f16 xs[NB * kMaxNormK];
@@ -257,12 +263,26 @@ __global__ __launch_bounds__(kNT) void rms_qkv_rope_append_kernel(QkvArgs a) {
   // lane b < NB finishes batch row b.
   const int be = lane < NB ? lane : 0;
   const int64_t slot = kPaged ? a.slots[be * a.slot_sb] : a.write_index[0];
-  const float bias0 = a.bias != nullptr ? (float)a.bias[r0] : 0.f;
-  const float bias1 = a.bias != nullptr ? (float)a.bias[r1] : 0.f;
-  const f16* cp = a.cos + be * a.cs_sb;
-  const f16* sp = a.sin + be * a.cs_sb;
-  const float cos_lo = (float)cp[dd], sin_lo = (float)sp[dd];
-  const float cos_hi = (float)cp[dd + 32], sin_hi = (float)sp[dd + 32];
+  // Branch-free bias: without one, a weight element is read and dropped (a
+  // guarded load would wait for completion before the weights go out).
+  const bool has_bias = a.bias != nullptr;
+  const f16* bsrc = has_bias ? a.bias : a.w;
+  const float braw0 = (float)bsrc[r0], braw1 = (float)bsrc[r1];
+  const float bias0 = has_bias ? braw0 : 0.f;
+  const float bias1 = has_bias ? braw1 : 0.f;
+  float cos_lo, sin_lo, cos_hi, sin_hi;
+  float ang = 0.f;
+  if (kPos) {
+    // Both halves of a rotate-half pair share frequency dd (emb = cat(f, f)).
+    ang = (float)a.pos[be] * a.inv_freq[dd];
+  } else {
+    const f16* cp = a.cos + be * a.cs_sb;
+    const f16* sp = a.sin + be * a.cs_sb;
+    cos_lo = (float)cp[dd];
+    sin_lo = (float)sp[dd];
+    cos_hi = (float)cp[dd + 32];
+    sin_hi = (float)sp[dd + 32];
+  }
   f16x8 w0[NS], w1[NS];
   load_row<NS>(a.w + (int64_t)r0 * K, C, w0, lane);
   load_row<NS>(a.w + (int64_t)r1 * K, C, w1, lane);
@@ -280,6 +300,12 @@ __global__ __launch_bounds__(kNT) void rms_qkv_rope_append_kernel(QkvArgs a) {
   } else {
     kro = be * a.kc_sb + slot * a.kc_sn;
     vro = be * a.vc_sb + slot * a.vc_sn;
+  }
+  if (kPos) {
+    // Evaluated while the weight rows are in flight (the angle's loads were
+    // issued before them).
+    cos_lo = cos_hi = (float)(f16)cosf(ang);
+    sin_lo = sin_hi = (float)(f16)sinf(ang);
   }
   f16* raw = (a.token != nullptr && blockIdx.x == 0) ? a.hidden_out : nullptr;
   rms_finish<NB>(st, K, a.eps, xs, red, raw, a.ho_sb);
@@ -668,10 +694,16 @@ __global__ __launch_bounds__(256) void argmax_step_kernel(FinArgs a) {
   __shared__ uint64_t part[kMaxB][256];
   const int tid = threadIdx.x;
   // Every load is issued before any wait: the keys, the step counter and
-  // (thread b) row b's position.
-  const int64_t s = a.step != nullptr ? a.step[0] : 0;
-  const int64_t p = (a.pos != nullptr && tid < a.B) ? a.pos[tid] : 0;
-  const int64_t wi = (a.write_index != nullptr && tid == 0) ? a.write_index[0] : 0;
+  // (thread b) row b's position.  The optional counters are read branch-free
+  // (a missing one reads a key and is dropped): a guarded load would wait for
+  // completion before the key loads go out.
+  const int64_t* keys64 = reinterpret_cast<const int64_t*>(a.keys);
+  const int64_t s_raw = (a.step != nullptr ? a.step : keys64)[0];
+  const int64_t p_raw = (a.pos != nullptr ? a.pos : keys64)[min(tid, a.B - 1)];
+  const int64_t w_raw = (a.write_index != nullptr ? a.write_index : keys64)[0];
+  const int64_t s = a.step != nullptr ? s_raw : 0;
+  const int64_t p = a.pos != nullptr ? p_raw : 0;
+  const int64_t wi = a.write_index != nullptr ? w_raw : 0;
   // Four keys per row per thread and round, all rows' loads issued together
   // (indices past n_blocks re-read the last key).
   uint64_t k[kMaxB];
@@ -734,11 +766,20 @@ static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) 
     default: hipLaunchKernelGGL((KERNEL<4, ##__VA_ARGS__>), grid, block, shm, st, a); break; \
   }
 
+// RoPE source of the QKV entry points: 0 = cos/sin tables, 1 = positions +
+// inv_freq, -1 = neither or a mix.
+static int rope_source(const void* cos, const void* sin, const int64_t* pos, const float* inv_freq) {
+  if (cos && sin && !pos && !inv_freq) return 0;
+  if (!cos && !sin && pos && inv_freq) return 1;
+  return -1;
+}
+
 extern "C" int qf_rms_qkv_rope_append(const void* x, int64_t x_sb, const int64_t* token,
                                       void* hidden_out, int64_t ho_sb,
                                       const void* norm_w, float eps,
                                       const void* w_qkv, const void* bias,
                                       const void* cos, const void* sin, int64_t cs_sb,
+                                      const int64_t* pos, const float* inv_freq,
                                       void* k_cache, int64_t kc_sb, int64_t kc_sh, int64_t kc_sn,
                                       void* v_cache, int64_t vc_sb, int64_t vc_sh, int64_t vc_sn,
                                       const int64_t* write_index,
@@ -747,8 +788,10 @@ extern "C" int qf_rms_qkv_rope_append(const void* x, int64_t x_sb, const int64_t
                                       void* stream) {
   if (D != kHeadDim) return QF_ERR_UNSUPPORTED;
   if (B < 1 || B > kMaxB || hidden < 8 || hidden > kMaxNormK || hidden % 8) return QF_ERR_UNSUPPORTED;
-  if (!x || !norm_w || !w_qkv || !cos || !sin || !k_cache || !v_cache || !write_index || !q_out)
+  if (!x || !norm_w || !w_qkv || !k_cache || !v_cache || !write_index || !q_out)
     return QF_ERR_INVALID_ARG;
+  const int rope_mode = rope_source(cos, sin, pos, inv_freq);
+  if (rope_mode < 0) return QF_ERR_INVALID_ARG;
   if (QH < 1 || KVH < 1 || cap < 1) return QF_ERR_INVALID_ARG;
   if (token != nullptr && hidden_out != nullptr && (!al16(hidden_out) || (ho_sb & 7)))
     return QF_ERR_INVALID_ARG;
@@ -760,6 +803,7 @@ extern "C" int qf_rms_qkv_rope_append(const void* x, int64_t x_sb, const int64_t
   a.norm_w = static_cast<const f16*>(norm_w); a.eps = eps;
   a.w = static_cast<const f16*>(w_qkv); a.bias = static_cast<const f16*>(bias);
   a.cos = static_cast<const f16*>(cos); a.sin = static_cast<const f16*>(sin); a.cs_sb = cs_sb;
+  a.pos = pos; a.inv_freq = inv_freq;
   a.kc = static_cast<f16*>(k_cache); a.kc_sb = kc_sb; a.kc_sh = kc_sh; a.kc_sn = kc_sn;
   a.vc = static_cast<f16*>(v_cache); a.vc_sb = vc_sb; a.vc_sh = vc_sh; a.vc_sn = vc_sn;
   a.write_index = write_index;
@@ -769,7 +813,11 @@ extern "C" int qf_rms_qkv_rope_append(const void* x, int64_t x_sb, const int64_t
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid((a.n_pairs + kNW - 1) / kNW), block(kNT);
   const size_t shm = 0;
-  QF_DISPATCH_B(B, rms_qkv_rope_append_kernel, false)
+  if (rope_mode == 1) {
+    QF_DISPATCH_B(B, rms_qkv_rope_append_kernel, false, true)
+  } else {
+    QF_DISPATCH_B(B, rms_qkv_rope_append_kernel, false, false)
+  }
   return (int)hipGetLastError();
 }
 
@@ -778,6 +826,7 @@ extern "C" int qf_rms_qkv_rope_append_paged(const void* x, int64_t x_sb, const i
                                             const void* norm_w, float eps,
                                             const void* w_qkv, const void* bias,
                                             const void* cos, const void* sin, int64_t cs_sb,
+                                            const int64_t* pos, const float* inv_freq,
                                             void* k_pool, int64_t kp_sp, int64_t kp_sh, int64_t kp_sn,
                                             void* v_pool, int64_t vp_sp, int64_t vp_sh, int64_t vp_sn,
                                             const int32_t* block_table, int64_t bt_sb,
@@ -789,9 +838,10 @@ extern "C" int qf_rms_qkv_rope_append_paged(const void* x, int64_t x_sb, const i
   const int l2 = page_log2(page_size, pages_per_row, n_pages);
   if (D != kHeadDim || l2 < 0) return QF_ERR_UNSUPPORTED;
   if (B < 1 || B > kMaxB || hidden < 8 || hidden > kMaxNormK || hidden % 8) return QF_ERR_UNSUPPORTED;
-  if (!x || !norm_w || !w_qkv || !cos || !sin || !k_pool || !v_pool || !block_table || !slots ||
-      !q_out)
+  if (!x || !norm_w || !w_qkv || !k_pool || !v_pool || !block_table || !slots || !q_out)
     return QF_ERR_INVALID_ARG;
+  const int rope_mode = rope_source(cos, sin, pos, inv_freq);
+  if (rope_mode < 0) return QF_ERR_INVALID_ARG;
   if (QH < 1 || KVH < 1 || bt_sb < pages_per_row) return QF_ERR_INVALID_ARG;
   if (token != nullptr && hidden_out != nullptr && (!al16(hidden_out) || (ho_sb & 7)))
     return QF_ERR_INVALID_ARG;
@@ -802,6 +852,7 @@ extern "C" int qf_rms_qkv_rope_append_paged(const void* x, int64_t x_sb, const i
   a.norm_w = static_cast<const f16*>(norm_w); a.eps = eps;
   a.w = static_cast<const f16*>(w_qkv); a.bias = static_cast<const f16*>(bias);
   a.cos = static_cast<const f16*>(cos); a.sin = static_cast<const f16*>(sin); a.cs_sb = cs_sb;
+  a.pos = pos; a.inv_freq = inv_freq;
   a.kc = static_cast<f16*>(k_pool); a.kc_sb = kp_sp; a.kc_sh = kp_sh; a.kc_sn = kp_sn;
   a.vc = static_cast<f16*>(v_pool); a.vc_sb = vp_sp; a.vc_sh = vp_sh; a.vc_sn = vp_sn;
   a.write_index = nullptr;
@@ -813,7 +864,11 @@ extern "C" int qf_rms_qkv_rope_append_paged(const void* x, int64_t x_sb, const i
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid((a.n_pairs + kNW - 1) / kNW), block(kNT);
   const size_t shm = 0;
-  QF_DISPATCH_B(B, rms_qkv_rope_append_kernel, true)
+  if (rope_mode == 1) {
+    QF_DISPATCH_B(B, rms_qkv_rope_append_kernel, true, true)
+  } else {
+    QF_DISPATCH_B(B, rms_qkv_rope_append_kernel, true, false)
+  }
   return (int)hipGetLastError();
 }
 

@@ -160,19 +160,21 @@ class DecodeEngine:
         eps = cfg.rms_eps
         if ctx["bias"] is not None:
             ctx["bias"].index_fill_(1, ctx["write"], 0.0)
-        cos, sin = cos_sin(ctx["pos"], self.inv_freq)          # (B, D), once per step (SE:910-915)
+        # RoPE angles from the positions inside the QKV kernel: the same fp16
+        # table as cos_sin (SE:910-915) without its separate launches.
+        rope = (ctx["pos"], self.inv_freq)
         hidden, q_rot, h = ctx["hidden"], ctx["q_rot"], ctx["h"]
         for i, (layer, (kc, vc)) in enumerate(zip(self.w["layers"], ctx["caches"])):
             if i == 0:
                 # Embedding gather (SE:896) folded into the first projection.
                 step_ops.rms_qkv_rope_append(self.w["embed"], layer["input_norm"], eps,
-                                             layer["qkv_weight"], layer["qkv_bias"], cos, sin,
+                                             layer["qkv_weight"], layer["qkv_bias"], None, None,
                                              kc, vc, ctx["write"], q_rot, token=ctx["token"],
-                                             hidden_out=hidden)
+                                             hidden_out=hidden, positions=rope)
             else:
                 step_ops.rms_qkv_rope_append(hidden, layer["input_norm"], eps, layer["qkv_weight"],
-                                             layer["qkv_bias"], cos, sin, kc, vc, ctx["write"],
-                                             q_rot)
+                                             layer["qkv_bias"], None, None, kc, vc, ctx["write"],
+                                             q_rot, positions=rope)
             grouped = q_rot.view(b, cfg.kv_heads, cfg.groups, cfg.head_dim)
             # Split-K partials; their merge is the o_proj kernel's prologue.
             ops.flash_decode_split(grouped, kc, vc, ctx["bias"], ctx["flash"],

@@ -25,7 +25,7 @@ import torch
 
 from . import _lib
 from .ops import HEAD_DIM, _ptr, _require_cuda_fp16, _scratch_args, _stream
-from .step_ops import _batch, _check, _rows, _weight
+from .step_ops import _batch, _check, _rows, _weight, rope_args
 
 MIN_PAGE, MAX_PAGE = 64, 4096
 
@@ -299,13 +299,15 @@ def prefill_varlen_paged(query: torch.Tensor, key: torch.Tensor, value: torch.Te
 
 
 def rms_qkv_rope_append_paged(x: torch.Tensor, norm_w: torch.Tensor, eps: float,
-                              w_qkv: torch.Tensor, bias: torch.Tensor | None, cos: torch.Tensor,
-                              sin: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                              w_qkv: torch.Tensor, bias: torch.Tensor | None,
+                              cos: torch.Tensor | None, sin: torch.Tensor | None,
+                              k_pool: torch.Tensor, v_pool: torch.Tensor,
                               block_table: torch.Tensor, slots: torch.Tensor,
                               q_out: torch.Tensor, token: torch.Tensor | None = None,
-                              hidden_out: torch.Tensor | None = None) -> None:
+                              hidden_out: torch.Tensor | None = None, positions=None) -> None:
     """``step_ops.rms_qkv_rope_append`` appending into paged caches at per-row
-    ``slots`` (B,) int64 (each row's own position)."""
+    ``slots`` (B,) int64; RoPE from cos/sin tables or ``positions =
+    (pos, inv_freq)`` as there."""
     _check("q_out", q_out)
     if q_out.dim() != 3 or q_out.shape[2] != HEAD_DIM or q_out.stride(2) != 1:
         raise ValueError(f"q_out must be (B, QH, 64) (got {tuple(q_out.shape)})")
@@ -320,9 +322,7 @@ def rms_qkv_rope_append_paged(x: torch.Tensor, norm_w: torch.Tensor, eps: float,
         _check("bias", bias)
         if tuple(bias.shape) != ((qh + 2 * kvh) * HEAD_DIM,) or not bias.is_contiguous():
             raise ValueError("bias must be contiguous ((QH + 2 KVH) * 64,)")
-    cs_sb = _rows("cos", cos, b, HEAD_DIM)
-    if _rows("sin", sin, b, HEAD_DIM) != cs_sb:
-        raise ValueError("cos and sin must share a row stride")
+    rope = rope_args(cos, sin, positions, b)
     slot = _slot_args(slots, b, q_out.device)
     if token is not None:
         _check("token", token, torch.int64)
@@ -339,8 +339,7 @@ def rms_qkv_rope_append_paged(x: torch.Tensor, norm_w: torch.Tensor, eps: float,
         hidden_out = None
     rc = _lib.load().qf_rms_qkv_rope_append_paged(
         x.data_ptr(), x_sb, _ptr(token), _ptr(hidden_out), ho_sb,
-        norm_w.data_ptr(), float(eps), w_qkv.data_ptr(), _ptr(bias),
-        cos.data_ptr(), sin.data_ptr(), cs_sb, *pool, *slot,
+        norm_w.data_ptr(), float(eps), w_qkv.data_ptr(), _ptr(bias), *rope, *pool, *slot,
         q_out.data_ptr(), q_out.stride(0), q_out.stride(1),
         b, hidden, qh, kvh, HEAD_DIM, _stream(x.device))
     _lib.check(rc, "qf_rms_qkv_rope_append_paged")

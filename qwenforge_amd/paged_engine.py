@@ -109,18 +109,18 @@ class PagedDecodeEngine(DecodeEngine):
         b = ctx["token"].shape[0]
         eps = cfg.rms_eps
         kv, table, pos = ctx["kv"], ctx["table"], ctx["pos"]
-        cos, sin = cos_sin(pos, self.inv_freq)                   # (B, D): each row's own position
+        rope = (pos, self.inv_freq)                              # each row's own position
         hidden, q_rot, h = ctx["hidden"], ctx["q_rot"], ctx["h"]
         for i, (layer, (kp, vp)) in enumerate(zip(self.w["layers"], kv.pools)):
             if i == 0:
                 paged.rms_qkv_rope_append_paged(self.w["embed"], layer["input_norm"], eps,
-                                                layer["qkv_weight"], layer["qkv_bias"], cos, sin,
+                                                layer["qkv_weight"], layer["qkv_bias"], None, None,
                                                 kp, vp, table, pos, q_rot, token=ctx["token"],
-                                                hidden_out=hidden)
+                                                hidden_out=hidden, positions=rope)
             else:
                 paged.rms_qkv_rope_append_paged(hidden, layer["input_norm"], eps,
-                                                layer["qkv_weight"], layer["qkv_bias"], cos, sin,
-                                                kp, vp, table, pos, q_rot)
+                                                layer["qkv_weight"], layer["qkv_bias"], None, None,
+                                                kp, vp, table, pos, q_rot, positions=rope)
             grouped = q_rot.view(b, cfg.kv_heads, cfg.groups, cfg.head_dim)
             # The slot just written is the row's last valid one.
             paged.flash_decode_split_paged(grouped, kp, vp, table, None, ctx["flash"], kv_last=pos,

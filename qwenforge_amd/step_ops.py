@@ -62,18 +62,42 @@ def _batch(b: int) -> None:
         raise ValueError(f"fused decode-step kernels take 1..{MAX_BATCH} rows (got {b})")
 
 
+def rope_args(cos, sin, positions, batch: int):
+    """ABI pieces (cos, sin, cs_sb, pos, inv_freq) of the two RoPE sources:
+    (B, 64) fp16 tables, or ``positions = (pos (B,) int64, inv_freq (32,)
+    fp32)`` from which the kernel forms the same tables itself."""
+    if positions is not None:
+        if cos is not None or sin is not None:
+            raise ValueError("pass cos/sin tables or positions, not both")
+        pos, inv = positions
+        _check("pos", pos, torch.int64)
+        _check("inv_freq", inv, torch.float32)
+        if pos.shape != (batch,) or not pos.is_contiguous():
+            raise ValueError("pos must be contiguous (B,)")
+        if inv.shape != (HEAD_DIM // 2,) or not inv.is_contiguous():
+            raise ValueError(f"inv_freq must be contiguous ({HEAD_DIM // 2},)")
+        return None, None, 0, pos.data_ptr(), inv.data_ptr()
+    if cos is None or sin is None:
+        raise ValueError("need cos and sin tables or positions")
+    cs_sb = _rows("cos", cos, batch, HEAD_DIM)
+    if _rows("sin", sin, batch, HEAD_DIM) != cs_sb:
+        raise ValueError("cos and sin must share a row stride")
+    return cos.data_ptr(), sin.data_ptr(), cs_sb, None, None
+
+
 def rms_qkv_rope_append(x: torch.Tensor, norm_w: torch.Tensor, eps: float, w_qkv: torch.Tensor,
-                        bias: torch.Tensor | None, cos: torch.Tensor, sin: torch.Tensor,
-                        key_cache: torch.Tensor, value_cache: torch.Tensor,
-                        write_index: torch.Tensor, q_out: torch.Tensor,
-                        token: torch.Tensor | None = None,
-                        hidden_out: torch.Tensor | None = None) -> None:
+                        bias: torch.Tensor | None, cos: torch.Tensor | None,
+                        sin: torch.Tensor | None, key_cache: torch.Tensor,
+                        value_cache: torch.Tensor, write_index: torch.Tensor,
+                        q_out: torch.Tensor, token: torch.Tensor | None = None,
+                        hidden_out: torch.Tensor | None = None, positions=None) -> None:
     """q_out <- RoPE(q); caches[:, :, write_index] <- RoPE(k), v.
 
     ``x`` is the (B, hidden) residual stream, or -- with ``token`` (B,) int64
     -- the (vocab, hidden) embedding table whose rows ``token`` are gathered
-    (and copied to ``hidden_out`` when given).  ``cos``/``sin``: (B, 64) fp16.
-    ``q_out``: (B, QH, 64) fp16.
+    (and copied to ``hidden_out`` when given).  RoPE from ``cos``/``sin``
+    (B, 64) fp16 tables, or from ``positions = (pos, inv_freq)`` (the kernel
+    forms the identical tables; cos/sin then None).  ``q_out``: (B, QH, 64).
     """
     b, kvh, cap, d = key_cache.shape
     _batch(b)
@@ -94,9 +118,7 @@ def rms_qkv_rope_append(x: torch.Tensor, norm_w: torch.Tensor, eps: float, w_qkv
         _check("bias", bias)
         if tuple(bias.shape) != ((qh + 2 * kvh) * d,) or not bias.is_contiguous():
             raise ValueError("bias must be contiguous ((QH + 2 KVH) * 64,)")
-    cs_sb = _rows("cos", cos, b, d)
-    if _rows("sin", sin, b, d) != cs_sb:
-        raise ValueError("cos and sin must share a row stride")
+    rope = rope_args(cos, sin, positions, b)
     _check("write_index", write_index, torch.int64)
     if token is not None:
         _check("token", token, torch.int64)
@@ -114,8 +136,7 @@ def rms_qkv_rope_append(x: torch.Tensor, norm_w: torch.Tensor, eps: float, w_qkv
     lib = _lib.load()
     rc = lib.qf_rms_qkv_rope_append(
         x.data_ptr(), x_sb, _ptr(token), _ptr(hidden_out), ho_sb,
-        norm_w.data_ptr(), float(eps), w_qkv.data_ptr(), _ptr(bias),
-        cos.data_ptr(), sin.data_ptr(), cs_sb,
+        norm_w.data_ptr(), float(eps), w_qkv.data_ptr(), _ptr(bias), *rope,
         key_cache.data_ptr(), *key_cache.stride()[:3],
         value_cache.data_ptr(), *value_cache.stride()[:3],
         write_index.data_ptr(), q_out.data_ptr(), q_out.stride(0), q_out.stride(1),

@@ -121,14 +121,16 @@ def test_step_kernels_reject_bad_arguments():
     assert lib.qf_rms_lm_head(16, 896, 16, 1e-6, 16, 16, 100, 16, 8, 0, 896, 100, None) == -2
     assert lib.qf_argmax_step(16, 8, 1, 16, 16, 4, 4, None, None, None, None) == -1  # rows w/o step
     assert lib.qf_argmax_step(16, 8, 9, 16, None, 0, 0, None, None, None, None) == -2
-    rc = lib.qf_rms_qkv_rope_append(16, 896, None, None, 0, 16, 1e-6, 16, None, 16, 16, 64,
-                                    16, 0, 0, 0, 16, 0, 0, 0, 16, 16, 0, 0,
-                                    1, 896, 14, 2, 128, 64, None)
-    assert rc == -2  # head_dim 128
-    rc = lib.qf_rms_qkv_rope_append(16, 896, None, None, 0, 16, 1e-6, 16, None, 16, 16, 64,
-                                    None, 0, 0, 0, 16, 0, 0, 0, 16, 16, 0, 0,
-                                    1, 896, 14, 2, 64, 64, None)
-    assert rc == -1  # no key cache
+    def qkv(cos=16, sin=16, pos=None, inv=None, kc=16, D=64):
+        return lib.qf_rms_qkv_rope_append(16, 896, None, None, 0, 16, 1e-6, 16, None, cos, sin, 64,
+                                          pos, inv, kc, 0, 0, 0, 16, 0, 0, 0, 16, 16, 0, 0,
+                                          1, 896, 14, 2, D, 64, None)
+
+    assert qkv(D=128) == -2                      # head_dim 128
+    assert qkv(kc=None) == -1                    # no key cache
+    assert qkv(pos=16, inv=16) == -1             # tables and positions together
+    assert qkv(cos=None, sin=None) == -1         # neither RoPE source
+    assert qkv(cos=None, sin=None, pos=16) == -1  # positions without inv_freq
 
 
 def test_prefill_workspace_plan():
@@ -201,7 +203,7 @@ def test_paged_entry_points_reject_bad_arguments():
 
     def qkv(page=64, slots=16, B=1):
         return lib.qf_rms_qkv_rope_append_paged(16, 896, None, None, 0, 16, 1e-6, 16, None,
-                                                16, 16, 64, 16, 8192, 4096, 64,
+                                                16, 16, 64, None, None, 16, 8192, 4096, 64,
                                                 16, 8192, 4096, 64, 16, 4, 4, 8, page,
                                                 slots, 1, 16, 896, 64, B, 896, 14, 2, 64, None)
 

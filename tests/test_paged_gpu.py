@@ -251,3 +251,34 @@ def test_rms_qkv_rope_append_paged_matches_dense(dev, batch):
     assert torch.equal(vp.cpu(), vp_ref)
     qo, ko, vo = ost.qkv_rope16(x, nw, 1e-6, w, bias, cos, sin, QH, KVH, D)
     assert ((q_out.float().cpu() - qo.float()).abs() / qo.float().abs().clamp_min(1)).max() <= 4e-3
+
+
+def test_rms_qkv_rope_append_paged_positions_mode(dev):
+    """Paged QKV append with in-kernel RoPE angles equals the table mode."""
+    from qwenforge_amd.rope import cos_sin, inv_freq as make_inv
+
+    gen = torch.Generator().manual_seed(44)
+    batch, hidden, width = 2, 896, (QH + 2 * KVH) * D
+    x = torch.randn(batch, hidden, generator=gen).half().to(dev)
+    nw = (torch.rand(hidden, generator=gen) + 0.5).half().to(dev)
+    w = (torch.randn(width, hidden, generator=gen) * 0.02).half().to(dev)
+    page, ppr = 64, 2
+    table = _table(gen, batch, ppr, batch * ppr).to(dev)
+    slots = torch.tensor([7, 100], device=dev)
+    inv = make_inv(D, 1e6, dev)
+    cos, sin = cos_sin(slots, inv)
+    outs = []
+    for use_pos in (False, True):
+        kp = torch.zeros(batch * ppr, KVH, page, D, device=dev, dtype=torch.float16)
+        vp = torch.zeros_like(kp)
+        q_out = torch.zeros(batch, QH, D, device=dev, dtype=torch.float16)
+        if use_pos:
+            paged.rms_qkv_rope_append_paged(x, nw, 1e-6, w, None, None, None, kp, vp, table, slots,
+                                            q_out, positions=(slots, inv))
+        else:
+            paged.rms_qkv_rope_append_paged(x, nw, 1e-6, w, None, cos, sin, kp, vp, table, slots,
+                                            q_out)
+        outs.append((q_out, kp, vp))
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a.cpu(), b.cpu())

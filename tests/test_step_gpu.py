@@ -242,3 +242,38 @@ def test_attn_merge_o_proj(dev, batch, splits):
     assert ok, err
     ok, err = _close(hidden, hidden2.cpu(), tol=2e-3)
     assert ok, err
+
+
+@pytest.mark.parametrize("batch", [1, 3, 4])
+def test_rms_qkv_rope_positions_mode_equals_table_mode(dev, batch):
+    """RoPE angles formed in the kernel from (pos, inv_freq) give exactly the
+    outputs of the torch-built fp16 tables (SE:910-915), including far
+    positions and a negative one."""
+    from qwenforge_amd.rope import cos_sin, inv_freq as make_inv
+
+    gen = torch.Generator().manual_seed(60 + batch)
+    width = (QH + 2 * KVH) * D
+    x = _rand(batch, HIDDEN, gen=gen).to(dev)
+    nw = (torch.rand(HIDDEN, generator=gen) + 0.5).to(torch.float16).to(dev)
+    w = _rand(width, HIDDEN, gen=gen, std=0.02).to(dev)
+    bias = _rand(width, gen=gen, std=0.1).to(dev)
+    pos = torch.tensor([0, 1023, 131071, -5][:batch], device=dev)
+    inv = make_inv(D, 1e6, dev)
+    cos, sin = cos_sin(pos, inv)
+    cap, slot = 64, 9
+    outs = []
+    for mode in ("table", "positions"):
+        kc = torch.zeros(batch, KVH, cap, D, device=dev, dtype=torch.float16)
+        vc = torch.zeros_like(kc)
+        q_out = torch.zeros(batch, QH, D, device=dev, dtype=torch.float16)
+        if mode == "table":
+            step_ops.rms_qkv_rope_append(x, nw, EPS, w, bias, cos, sin, kc, vc,
+                                         torch.tensor([slot], device=dev), q_out)
+        else:
+            step_ops.rms_qkv_rope_append(x, nw, EPS, w, bias, None, None, kc, vc,
+                                         torch.tensor([slot], device=dev), q_out,
+                                         positions=(pos, inv))
+        outs.append((q_out, kc, vc))
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.equal(a.cpu(), b.cpu())
