@@ -893,11 +893,24 @@ extern "C" int qf_gemv_residual(const void* inp, int64_t in_sb, const void* w, v
     if (B * C <= kNT) { QF_DISPATCH_B(B, gemv_residual_kernel, 2, 2, 1) }
     else { QF_DISPATCH_B(B, gemv_residual_kernel, 2, 2, 2) }
   } else {
-    // Long rows (down_proj): one row per wave, the whole row in flight.
+    // Long rows (down_proj): one row per wave, the whole row in flight, with
+    // as many 64-lane chunk rounds as the row needs (10 for K = 4864).
     const dim3 grid((N + kNW - 1) / kNW);
-    if (B * C <= 4 * kNT) { QF_DISPATCH_B(B, gemv_residual_kernel, 16, 1, 4) }
-    else if (B * C <= 8 * kNT) { QF_DISPATCH_B(B, gemv_residual_kernel, 16, 1, 8) }
-    else { QF_DISPATCH_B(B, gemv_residual_kernel, 16, 1, 16) }
+    const int ns = (C + 63) / 64;
+    // XP: 16-byte input chunks staged per thread (B * C <= XP * kNT).
+    if (ns <= 10) {
+      if (B * C <= 4 * kNT) { QF_DISPATCH_B(B, gemv_residual_kernel, 10, 1, 4) }
+      else if (B * C <= 8 * kNT) { QF_DISPATCH_B(B, gemv_residual_kernel, 10, 1, 8) }
+      else { QF_DISPATCH_B(B, gemv_residual_kernel, 10, 1, 16) }
+    } else if (ns <= 12) {
+      if (B * C <= 4 * kNT) { QF_DISPATCH_B(B, gemv_residual_kernel, 12, 1, 4) }
+      else if (B * C <= 8 * kNT) { QF_DISPATCH_B(B, gemv_residual_kernel, 12, 1, 8) }
+      else { QF_DISPATCH_B(B, gemv_residual_kernel, 12, 1, 16) }
+    } else {
+      if (B * C <= 4 * kNT) { QF_DISPATCH_B(B, gemv_residual_kernel, 16, 1, 4) }
+      else if (B * C <= 8 * kNT) { QF_DISPATCH_B(B, gemv_residual_kernel, 16, 1, 8) }
+      else { QF_DISPATCH_B(B, gemv_residual_kernel, 16, 1, 16) }
+    }
   }
   return (int)hipGetLastError();
 }
