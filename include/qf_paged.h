@@ -122,7 +122,7 @@ int qf_prefill_varlen_paged(const void* q, int64_t q_sh, int64_t q_sn,
 int qf_rms_qkv_rope_append_paged(const void* x, int64_t x_sb, const int64_t* token,
                                  void* hidden_out, int64_t ho_sb,
                                  const void* norm_w, float eps,
-                                 const void* w_qkv, const void* bias,
+                                 const void* w_qkv, int w_layout, const void* bias,
                                  const void* cos, const void* sin, int64_t cs_sb,
                                  const int64_t* pos, const float* inv_freq,
                                  void* k_pool, int64_t kp_sp, int64_t kp_sh, int64_t kp_sn,

@@ -25,6 +25,28 @@
 extern "C" {
 #endif
 
+/* Weight layouts accepted by the projection entry points (w_layout):
+ *   QF_W_ROWS   torch Linear layout, (out, in) row-major -- the VALU kernels;
+ *   QF_W_TILES  matrix-core tiles written by qf_pack_weight with the row map
+ *               the entry point names -- the MFMA kernels (in % 32 == 0). */
+#define QF_W_ROWS 0
+#define QF_W_TILES 1
+
+/* Row maps of qf_pack_weight. */
+#define QF_PACK_PLAIN 0   /* o_proj, down_proj, lm_head */
+#define QF_PACK_SWIGLU 1  /* gate_up_weight: gate rows [0, N/2), up rows [N/2, N) */
+#define QF_PACK_ROPE 2    /* qkv_weight: 64-row heads, rotate-half pairs (d, d + 32) */
+
+/* Repack a projection weight W (N, K) fp16, row stride w_sb, into matrix-core
+ * tiles: tile (rb, kb) of 16 rows x 32 k is 1 KB at (rb * K/32 + kb) * 1 KB,
+ * lane l's 16 bytes being W[row(rb, l % 16)][32 kb + 8 (l / 16) .. +7].  The
+ * row map (layout) is QF_PACK_PLAIN (row 16 rb + r), QF_PACK_SWIGLU or
+ * QF_PACK_ROPE (see decode_step.hip).  No counterpart in the reference: it is
+ * the one-time load step that lets every decode-step weight load be a
+ * contiguous 1 KB read.  N % 16 == 0 (% 64 for ROPE), K % 32 == 0. */
+int qf_pack_weight(const void* w, int64_t w_sb, void* packed, int N, int K, int layout,
+                   void* stream);
+
 /* RMSNorm + fused QKV projection (+ bias) + rotate-half RoPE + KV append.
  * Replaces student_engine.py:917-932 (rms_norm, F.linear(normalized,
  * qkv_weight, qkv_bias), split, the eager RoPE of q and k with the per-step
@@ -34,7 +56,9 @@ extern "C" {
  * non-null, row b is taken from x + token[b] * x_sb instead (x is then the
  * embedding table, :896) and, if `hidden_out` is non-null, the gathered rows
  * are also written to hidden_out (row stride ho_sb) as the residual stream.
- * w_qkv: ((QH + 2*KVH) * 64, hidden); bias: (QH + 2*KVH) * 64 or null.
+ * w_qkv: ((QH + 2*KVH) * 64, hidden) as rows (w_layout QF_W_ROWS) or packed
+ * with QF_PACK_ROPE (QF_W_TILES, hidden % 32 == 0); bias: (QH + 2*KVH) * 64
+ * or null.
  * RoPE angles come from either cos/sin: (B, 64) fp16 tables, row stride
  * cs_sb (pos and inv_freq NULL), or pos: (B,) int64 positions plus inv_freq:
  * (32,) fp32 (cos and sin NULL), in which case the table entries
@@ -48,7 +72,7 @@ extern "C" {
 int qf_rms_qkv_rope_append(const void* x, int64_t x_sb, const int64_t* token,
                            void* hidden_out, int64_t ho_sb,
                            const void* norm_w, float eps,
-                           const void* w_qkv, const void* bias,
+                           const void* w_qkv, int w_layout, const void* bias,
                            const void* cos, const void* sin, int64_t cs_sb,
                            const int64_t* pos, const float* inv_freq,
                            void* k_cache, int64_t kc_sb, int64_t kc_sh, int64_t kc_sn,
@@ -83,10 +107,12 @@ int qf_attn_merge_o_proj(const float* acc, const float* m, const float* l, int s
  * rms_norm(hidden, post_norm)` (:976-977) and the first two lines of _mlp
  * (:664-665) plus the product `gate * up` (:666): h = fp16(fp16(silu(g)) * u)
  * with g = fp16(acc_gate), u = fp16(acc_up).  w_gate_up: (2*I, hidden) with
- * the gate rows first (the reference's fused layout, :520-527); h_out: (B, I)
- * row stride ho_sb.  Supports hidden <= 1024, B in 1..4. */
+ * the gate rows first (the reference's fused layout, :520-527) as rows
+ * (QF_W_ROWS) or packed with QF_PACK_SWIGLU (QF_W_TILES, I % 8 == 0,
+ * hidden % 32 == 0); h_out: (B, I) row stride ho_sb.  Supports hidden <= 1024,
+ * B in 1..4. */
 int qf_rms_gate_up_swiglu(const void* x, int64_t x_sb, const void* norm_w, float eps,
-                          const void* w_gate_up, void* h_out, int64_t ho_sb,
+                          const void* w_gate_up, int w_layout, void* h_out, int64_t ho_sb,
                           int B, int hidden, int I, void* stream);
 
 /* Final RMSNorm + lm_head projection + per-block argmax.  Replaces

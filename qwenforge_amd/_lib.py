@@ -101,7 +101,7 @@ SIGNATURES = {
         _vp, _i64, _vp,                 # x, x_sb, token
         _vp, _i64,                      # hidden_out, ho_sb
         _vp, _f32,                      # norm_w, eps
-        _vp, _vp,                       # w_qkv, bias
+        _vp, _i32, _vp,                 # w_qkv, w_layout, bias
         _vp, _vp, _i64,                 # cos, sin, cs_sb
         _vp, _vp,                       # pos, inv_freq
         _vp, _i64, _i64, _i64,          # k_cache
@@ -126,7 +126,7 @@ SIGNATURES = {
     ],
     "qf_rms_gate_up_swiglu": [
         _vp, _i64, _vp, _f32,           # x, x_sb, norm_w, eps
-        _vp, _vp, _i64,                 # w_gate_up, h_out, ho_sb
+        _vp, _i32, _vp, _i64,           # w_gate_up, w_layout, h_out, ho_sb
         _i32, _i32, _i32,               # B, hidden, I
         _vp,                            # stream
     ],
@@ -198,7 +198,7 @@ SIGNATURES = {
         _vp, _i64, _vp,                 # x, x_sb, token
         _vp, _i64,                      # hidden_out, ho_sb
         _vp, _f32,                      # norm_w, eps
-        _vp, _vp,                       # w_qkv, bias
+        _vp, _i32, _vp,                 # w_qkv, w_layout, bias
         _vp, _vp, _i64,                 # cos, sin, cs_sb
         _vp, _vp,                       # pos, inv_freq
         _vp, _i64, _i64, _i64,          # k_pool
@@ -207,6 +207,11 @@ SIGNATURES = {
         _vp, _i64,                      # slots, slot_sb
         _vp, _i64, _i64,                # q_out, qo_sb, qo_sh
         _i32, _i32, _i32, _i32, _i32,   # B, hidden, QH, KVH, D
+        _vp,                            # stream
+    ],
+    "qf_pack_weight": [
+        _vp, _i64, _vp,                 # w, w_sb, packed
+        _i32, _i32, _i32,               # N, K, layout
         _vp,                            # stream
     ],
     "qf_error_string": [_i32],

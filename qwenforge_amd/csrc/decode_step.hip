@@ -582,6 +582,248 @@ __global__ __launch_bounds__(kNT) void rms_gate_up_swiglu_kernel(GateUpArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Matrix-core forms (weights packed by qf_pack_weight).  The NB batch rows
+// are the columns of a v_mfma_f32_16x16x32_f16 (columns >= NB are zero) and
+// 16 weight rows its A operand, so the k-reduction happens inside the matrix
+// core: no cross-lane sums, and one 16-byte LDS activation read per lane per
+// 32 k (the VALU form reads NB per weight row).  A packed tile (row block rb,
+// k block kb) is the 1 KB A operand in lane order -- lane l's 16 bytes are
+// row r = l % 16, k = 32 kb + 8 (l / 16) .. +7 -- so every weight load of a
+// wave is one contiguous 1 KB read.  Tiles are stored rb-major.
+__device__ __forceinline__ f16x8 tile_load(const f16* __restrict__ w, int nkb, int rb, int kb,
+                                           int lane) {
+  return load16(w + (((int64_t)rb * nkb + kb) * 64 + lane) * 8);
+}
+
+// B operand of k block kb for lane l: staged activation row l % 16 at
+// k = 32 kb + 8 (l / 16), zero for columns >= NB.
+template <int NB>
+__device__ __forceinline__ f16x8 act_operand(const f16* xs, int K, int kb, int lane) {
+  const int col = lane & 15;
+  const f16x8 v = *reinterpret_cast<const f16x8*>(xs + min(col, NB - 1) * K + 32 * kb +
+                                                   8 * (lane >> 4));
+  return col < NB ? v : zero8();
+}
+
+// The MFMA k blocks of one wave: blocks [kb0, kb0 + n) (n <= NBLK) of a
+// row block, with the tile loads issued by the caller beforehand.
+template <int NB, int NBLK>
+__device__ __forceinline__ f32x4 tile_mfma(const f16x8 (&wa)[NBLK], const f16* xs, int K, int kb0,
+                                           int n, int lane) {
+  // Every B operand is read from LDS before the first MFMA, so the LDS
+  // latency is paid once, not once per block.
+  f16x8 xb[NBLK];
+#pragma unroll
+  for (int t = 0; t < NBLK; ++t) xb[t] = t < n ? act_operand<NB>(xs, K, kb0 + t, lane) : zero8();
+  f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < NBLK; ++t) {
+    if (t & 1) acc1 = mfma16x16x32(wa[t], xb[t], acc1);
+    else acc0 = mfma16x16x32(wa[t], xb[t], acc0);
+  }
+  return acc0 + acc1;
+}
+
+// Gate/up + SwiGLU.  Packing QF_PACK_SWIGLU puts, in row block rb, MFMA
+// row r = 4g + i on gate row 8 rb + 2g + (i & 1) for i < 2 and on the
+// matching up row (+ I) for i >= 2, so C registers t (gate) and t + 2 (up)
+// of lane l are one SwiGLU pair: lane l finishes outputs 8 rb + 2 (l >> 4)
+// + {0, 1} of batch row l & 15.  KS waves split a row block's k range and
+// add their partial tiles in LDS.
+constexpr int kGuKS = 4;                             // k splits per row block
+constexpr int kGuBlk = kMaxNormK / 32 / kGuKS;       // k blocks per wave (max)
+
+template <int NB>
+__global__ __launch_bounds__(kNT) void rms_gate_up_swiglu_mfma_kernel(GateUpArgs a) {
+  __shared__ __attribute__((aligned(16))) f16 xs[NB * kMaxNormK];
+  __shared__ float red[kNW * NB];
+  __shared__ f32x4 part[kNW][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int K = a.K, nkb = K / 32;
+  const int per = (nkb + kGuKS - 1) / kGuKS;
+  const int kp = w % kGuKS;
+  const int nrb = a.I / 8;
+  const int rb = min((int)blockIdx.x * (kNW / kGuKS) + w / kGuKS, nrb - 1);
+  const int kb0 = kp * per, n = min(per, nkb - kb0);
+  const f16* rows[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) rows[b] = a.x + b * a.x_sb;
+  RmsStage<NB> st;
+  rms_load<NB>(st, rows, K, a.norm_w);
+  f16x8 wa[kGuBlk];
+#pragma unroll
+  for (int t = 0; t < kGuBlk; ++t) wa[t] = tile_load(a.w, nkb, rb, min(kb0 + t, nkb - 1), lane);
+  rms_finish<NB>(st, K, a.eps, xs, red, nullptr, 0);
+  f32x4 acc = tile_mfma<NB, kGuBlk>(wa, xs, K, kb0, n, lane);
+  if (kp != 0) part[w][lane] = acc;
+  __syncthreads();
+  if (kp != 0) return;
+#pragma unroll
+  for (int s = 1; s < kGuKS; ++s) acc += part[w + s][lane];
+  const int col = lane & 15;
+  const int jb = ((int)blockIdx.x * (kNW / kGuKS) + w / kGuKS) * 8 + 2 * (lane >> 4);
+  if (col >= NB || jb >= a.I) return;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    // F.silu on the fp16 gate (fp32 math, one rounding), then the fp16 product.
+    const float g16 = (float)(f16)acc[t], u16 = (float)(f16)acc[t + 2];
+    const float s16 = (float)(f16)(g16 / (1.f + expf(-g16)));
+    a.h[col * a.h_sb + jb + t] = (f16)(s16 * u16);
+  }
+}
+
+// QKV + bias + RoPE + KV append.  Packing QF_PACK_ROPE makes row block
+// rb = 4 head + c hold, in MFMA row r = 4g + i, row 64 head + d (i < 2) and
+// row 64 head + d + 32 (i >= 2) with d = 8c + 2g + (i & 1): lane l's C
+// registers t and t + 2 are the rotate-half pair of d = 8c + 2 (l >> 4) + t
+// for batch row l & 15, so bias, RoPE and the append run in the lane.
+constexpr int kQkvKS = 4;
+constexpr int kQkvBlk = kMaxNormK / 32 / kQkvKS;
+
+template <int NB, bool kPaged, bool kPos>
+__global__ __launch_bounds__(kNT) void rms_qkv_rope_append_mfma_kernel(QkvArgs a) {
+  __shared__ __attribute__((aligned(16))) f16 xs[NB * kMaxNormK];
+  __shared__ float red[kNW * NB];
+  __shared__ f32x4 part[kNW][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int K = a.K, nkb = K / 32;
+  const int per = (nkb + kQkvKS - 1) / kQkvKS;
+  const int kp = w % kQkvKS;
+  const int nrb = (a.QH + 2 * a.KVH) * 4;
+  const int rb = min((int)blockIdx.x * (kNW / kQkvKS) + w / kQkvKS, nrb - 1);
+  const int kb0 = kp * per, n = min(per, nkb - kb0);
+  const f16* rows[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+    rows[b] = a.x + (a.token != nullptr ? a.token[b] : (int64_t)b) * a.x_sb;
+  RmsStage<NB> st;
+  rms_load<NB>(st, rows, K, a.norm_w);
+  // Epilogue operands, loaded now so their latency hides under the weights'.
+  const int col = lane & 15, q = lane >> 4;
+  const int be = min(col, NB - 1);
+  const int head = rb >> 2;
+  const int d0 = 8 * (rb & 3) + 2 * q;  // this lane's pair dims d0, d0 + 1 (and + 32)
+  const int64_t slot = kPaged ? a.slots[be * a.slot_sb] : a.write_index[0];
+  // Branch-free bias: without one, a weight element is read and dropped.
+  const bool has_bias = a.bias != nullptr;
+  const f16* bsrc = (has_bias ? a.bias : a.w) + 64 * head + d0;
+  float bias[2][2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const float lo = (float)bsrc[t], hi = (float)bsrc[t + 32];
+    bias[t][0] = has_bias ? lo : 0.f;
+    bias[t][1] = has_bias ? hi : 0.f;
+  }
+  float cs[2][4];  // per dim: cos_lo, sin_lo, cos_hi, sin_hi
+  float ang[2] = {0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    if (kPos) {
+      ang[t] = (float)a.pos[be] * a.inv_freq[d0 + t];
+    } else {
+      const f16* cp = a.cos + be * a.cs_sb + d0 + t;
+      const f16* sp = a.sin + be * a.cs_sb + d0 + t;
+      cs[t][0] = (float)cp[0];
+      cs[t][1] = (float)sp[0];
+      cs[t][2] = (float)cp[32];
+      cs[t][3] = (float)sp[32];
+    }
+  }
+  f16x8 wa[kQkvBlk];
+#pragma unroll
+  for (int t = 0; t < kQkvBlk; ++t) wa[t] = tile_load(a.w, nkb, rb, min(kb0 + t, nkb - 1), lane);
+  // Destination slot offsets (kv head 0); the page lookup depends on the
+  // slot, so it is issued after the weights.
+  bool in_range = slot >= 0 && slot < a.cap;
+  int64_t kro, vro;
+  if (kPaged) {
+    const int64_t sl = in_range ? slot : 0;
+    const int page = a.table[be * a.t_sb + (sl >> a.log2p)];
+    in_range = in_range && page >= 0 && page < a.n_pages;
+    const int64_t prow = sl & ((1 << a.log2p) - 1);
+    kro = (int64_t)page * a.kc_sb + prow * a.kc_sn;
+    vro = (int64_t)page * a.vc_sb + prow * a.vc_sn;
+  } else {
+    kro = be * a.kc_sb + slot * a.kc_sn;
+    vro = be * a.vc_sb + slot * a.vc_sn;
+  }
+  if (kPos) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      cs[t][0] = cs[t][2] = (float)(f16)cosf(ang[t]);
+      cs[t][1] = cs[t][3] = (float)(f16)sinf(ang[t]);
+    }
+  }
+  f16* raw = (a.token != nullptr && blockIdx.x == 0) ? a.hidden_out : nullptr;
+  rms_finish<NB>(st, K, a.eps, xs, red, raw, a.ho_sb);
+  f32x4 acc = tile_mfma<NB, kQkvBlk>(wa, xs, K, kb0, n, lane);
+  if (kp != 0) part[w][lane] = acc;
+  __syncthreads();
+  if (kp != 0) return;
+#pragma unroll
+  for (int s = 1; s < kQkvKS; ++s) acc += part[w + s][lane];
+  const int rb_raw = (int)blockIdx.x * (kNW / kQkvKS) + w / kQkvKS;
+  if (col >= NB || rb_raw >= nrb) return;
+  const int b = col;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int d = d0 + t;
+    const float lo = (float)(f16)(acc[t] + bias[t][0]);
+    const float hi = (float)(f16)(acc[t + 2] + bias[t][1]);
+    if (head < a.QH + a.KVH) {
+      f16 olo, ohi;
+      rope1(lo, hi, cs[t][0], cs[t][1], cs[t][2], cs[t][3], olo, ohi);
+      if (head < a.QH) {
+        f16* qo = a.q_out + b * a.qo_sb + head * a.qo_sh;
+        qo[d] = olo;
+        qo[d + 32] = ohi;
+      } else if (in_range) {
+        f16* kd = a.kc + kro + (head - a.QH) * a.kc_sh;
+        kd[d] = olo;
+        kd[d + 32] = ohi;
+      }
+    } else if (in_range) {
+      f16* vd = a.vc + vro + (head - a.QH - a.KVH) * a.vc_sh;
+      vd[d] = (f16)lo;
+      vd[d + 32] = (f16)hi;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Weight packing (one pass at load time): tile (rb, kb), lane l, 16 bytes =
+// W[row(rb, l % 16)][32 kb + 8 (l / 16) ..].  Row maps: plain rows 16 rb + r;
+// QF_PACK_SWIGLU as above; QF_PACK_ROPE puts row block rb = 4 head + c on
+// rows 64 head + 8c + 2g + (i & 1) (+ 32 for i >= 2), pairing each
+// rotate-half (d, d + 32) in one lane's C registers.
+__device__ __forceinline__ int pack_row(int layout, int N, int rb, int r) {
+  const int g = r >> 2, i = r & 3;
+  if (layout == QF_PACK_SWIGLU) {
+    const int j = 8 * rb + 2 * g + (i & 1);
+    return (i & 2) ? N / 2 + j : j;
+  }
+  if (layout == QF_PACK_ROPE) {
+    const int head = rb >> 2, c = rb & 3;
+    return 64 * head + 8 * c + 2 * g + (i & 1) + ((i & 2) ? 32 : 0);
+  }
+  return 16 * rb + r;
+}
+
+__global__ __launch_bounds__(256) void pack_weight_kernel(const f16* __restrict__ w, int64_t w_sb,
+                                                          f16* __restrict__ out, int N, int K,
+                                                          int layout) {
+  const int nkb = K / 32;
+  const int64_t chunk = (int64_t)blockIdx.x * 256 + threadIdx.x;  // one 16-byte chunk
+  const int64_t total = (int64_t)(N / 16) * nkb * 64;
+  if (chunk >= total) return;
+  const int lane = (int)(chunk & 63);
+  const int64_t tile = chunk >> 6;
+  const int rb = (int)(tile / nkb), kb = (int)(tile % nkb);
+  const int row = pack_row(layout, N, rb, lane & 15);
+  store16(out + chunk * 8, load16(w + row * w_sb + 32 * kb + 8 * (lane >> 4)));
+}
+
+// ---------------------------------------------------------------------------
 struct LmArgs {
   const f16* x;
   int64_t x_sb;
@@ -766,6 +1008,21 @@ static bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) 
     default: hipLaunchKernelGGL((KERNEL<4, ##__VA_ARGS__>), grid, block, shm, st, a); break; \
   }
 
+extern "C" int qf_pack_weight(const void* w, int64_t w_sb, void* packed, int N, int K, int layout,
+                              void* stream) {
+  if (layout != QF_PACK_PLAIN && layout != QF_PACK_SWIGLU && layout != QF_PACK_ROPE)
+    return QF_ERR_INVALID_ARG;
+  if (N < 16 || N % 16 || K < 32 || K % 32) return QF_ERR_UNSUPPORTED;
+  if (layout == QF_PACK_ROPE && N % 64) return QF_ERR_UNSUPPORTED;
+  if (!w || !packed || w_sb < K || (w_sb & 7) || !al16(w) || !al16(packed)) return QF_ERR_INVALID_ARG;
+  const int64_t chunks = (int64_t)N * K / 8;
+  if ((chunks + 255) / 256 > 0x7fffffff) return QF_ERR_INVALID_ARG;
+  hipLaunchKernelGGL(pack_weight_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const f16*>(w), w_sb,
+                     static_cast<f16*>(packed), N, K, layout);
+  return (int)hipGetLastError();
+}
+
 // RoPE source of the QKV entry points: 0 = cos/sin tables, 1 = positions +
 // inv_freq, -1 = neither or a mix.
 static int rope_source(const void* cos, const void* sin, const int64_t* pos, const float* inv_freq) {
@@ -777,7 +1034,7 @@ static int rope_source(const void* cos, const void* sin, const int64_t* pos, con
 extern "C" int qf_rms_qkv_rope_append(const void* x, int64_t x_sb, const int64_t* token,
                                       void* hidden_out, int64_t ho_sb,
                                       const void* norm_w, float eps,
-                                      const void* w_qkv, const void* bias,
+                                      const void* w_qkv, int w_layout, const void* bias,
                                       const void* cos, const void* sin, int64_t cs_sb,
                                       const int64_t* pos, const float* inv_freq,
                                       void* k_cache, int64_t kc_sb, int64_t kc_sh, int64_t kc_sn,
@@ -786,6 +1043,7 @@ extern "C" int qf_rms_qkv_rope_append(const void* x, int64_t x_sb, const int64_t
                                       void* q_out, int64_t qo_sb, int64_t qo_sh,
                                       int B, int hidden, int QH, int KVH, int D, int cap,
                                       void* stream) {
+  if (w_layout != QF_W_ROWS && w_layout != QF_W_TILES) return QF_ERR_INVALID_ARG;
   if (D != kHeadDim) return QF_ERR_UNSUPPORTED;
   if (B < 1 || B > kMaxB || hidden < 8 || hidden > kMaxNormK || hidden % 8) return QF_ERR_UNSUPPORTED;
   if (!x || !norm_w || !w_qkv || !k_cache || !v_cache || !write_index || !q_out)
@@ -813,7 +1071,16 @@ extern "C" int qf_rms_qkv_rope_append(const void* x, int64_t x_sb, const int64_t
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid((a.n_pairs + kNW - 1) / kNW), block(kNT);
   const size_t shm = 0;
-  if (rope_mode == 1) {
+  if (w_layout == QF_W_TILES) {
+    if (hidden % 32) return QF_ERR_UNSUPPORTED;
+    const dim3 tgrid(((QH + 2 * KVH) * 4 + kNW / kQkvKS - 1) / (kNW / kQkvKS));
+    const dim3& grid = tgrid;
+    if (rope_mode == 1) {
+      QF_DISPATCH_B(B, rms_qkv_rope_append_mfma_kernel, false, true)
+    } else {
+      QF_DISPATCH_B(B, rms_qkv_rope_append_mfma_kernel, false, false)
+    }
+  } else if (rope_mode == 1) {
     QF_DISPATCH_B(B, rms_qkv_rope_append_kernel, false, true)
   } else {
     QF_DISPATCH_B(B, rms_qkv_rope_append_kernel, false, false)
@@ -824,7 +1091,7 @@ extern "C" int qf_rms_qkv_rope_append(const void* x, int64_t x_sb, const int64_t
 extern "C" int qf_rms_qkv_rope_append_paged(const void* x, int64_t x_sb, const int64_t* token,
                                             void* hidden_out, int64_t ho_sb,
                                             const void* norm_w, float eps,
-                                            const void* w_qkv, const void* bias,
+                                            const void* w_qkv, int w_layout, const void* bias,
                                             const void* cos, const void* sin, int64_t cs_sb,
                                             const int64_t* pos, const float* inv_freq,
                                             void* k_pool, int64_t kp_sp, int64_t kp_sh, int64_t kp_sn,
@@ -835,6 +1102,7 @@ extern "C" int qf_rms_qkv_rope_append_paged(const void* x, int64_t x_sb, const i
                                             void* q_out, int64_t qo_sb, int64_t qo_sh,
                                             int B, int hidden, int QH, int KVH, int D,
                                             void* stream) {
+  if (w_layout != QF_W_ROWS && w_layout != QF_W_TILES) return QF_ERR_INVALID_ARG;
   const int l2 = page_log2(page_size, pages_per_row, n_pages);
   if (D != kHeadDim || l2 < 0) return QF_ERR_UNSUPPORTED;
   if (B < 1 || B > kMaxB || hidden < 8 || hidden > kMaxNormK || hidden % 8) return QF_ERR_UNSUPPORTED;
@@ -864,7 +1132,16 @@ extern "C" int qf_rms_qkv_rope_append_paged(const void* x, int64_t x_sb, const i
   hipStream_t st = static_cast<hipStream_t>(stream);
   const dim3 grid((a.n_pairs + kNW - 1) / kNW), block(kNT);
   const size_t shm = 0;
-  if (rope_mode == 1) {
+  if (w_layout == QF_W_TILES) {
+    if (hidden % 32) return QF_ERR_UNSUPPORTED;
+    const dim3 tgrid(((QH + 2 * KVH) * 4 + kNW / kQkvKS - 1) / (kNW / kQkvKS));
+    const dim3& grid = tgrid;
+    if (rope_mode == 1) {
+      QF_DISPATCH_B(B, rms_qkv_rope_append_mfma_kernel, true, true)
+    } else {
+      QF_DISPATCH_B(B, rms_qkv_rope_append_mfma_kernel, true, false)
+    }
+  } else if (rope_mode == 1) {
     QF_DISPATCH_B(B, rms_qkv_rope_append_kernel, true, true)
   } else {
     QF_DISPATCH_B(B, rms_qkv_rope_append_kernel, true, false)
@@ -941,8 +1218,9 @@ extern "C" int qf_attn_merge_o_proj(const float* acc, const float* m, const floa
 }
 
 extern "C" int qf_rms_gate_up_swiglu(const void* x, int64_t x_sb, const void* norm_w, float eps,
-                                     const void* w_gate_up, void* h_out, int64_t ho_sb,
-                                     int B, int hidden, int I, void* stream) {
+                                     const void* w_gate_up, int w_layout, void* h_out,
+                                     int64_t ho_sb, int B, int hidden, int I, void* stream) {
+  if (w_layout != QF_W_ROWS && w_layout != QF_W_TILES) return QF_ERR_INVALID_ARG;
   if (B < 1 || B > kMaxB || hidden < 8 || hidden > kMaxNormK || hidden % 8) return QF_ERR_UNSUPPORTED;
   if (!x || !norm_w || !w_gate_up || !h_out || I < 1) return QF_ERR_INVALID_ARG;
   if (!al16(x) || !al16(norm_w) || !al16(w_gate_up) || (x_sb & 7)) return QF_ERR_INVALID_ARG;
@@ -953,10 +1231,18 @@ extern "C" int qf_rms_gate_up_swiglu(const void* x, int64_t x_sb, const void* no
   a.h = static_cast<f16*>(h_out); a.h_sb = ho_sb;
   a.K = hidden; a.I = I;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  constexpr int PW = 2;
-  const dim3 grid((I + kNW * PW - 1) / (kNW * PW)), block(kNT);
+  const dim3 block(kNT);
   const size_t shm = 0;
-  QF_DISPATCH_B(B, rms_gate_up_swiglu_kernel, PW)
+  if (w_layout == QF_W_TILES) {
+    // 8 SwiGLU pairs per row block, kNW / kGuKS row blocks per workgroup.
+    if (hidden % 32 || I % 8) return QF_ERR_UNSUPPORTED;
+    const dim3 grid((I / 8 + kNW / kGuKS - 1) / (kNW / kGuKS));
+    QF_DISPATCH_B(B, rms_gate_up_swiglu_mfma_kernel)
+  } else {
+    constexpr int PW = 2;
+    const dim3 grid((I + kNW * PW - 1) / (kNW * PW));
+    QF_DISPATCH_B(B, rms_gate_up_swiglu_kernel, PW)
+  }
   return (int)hipGetLastError();
 }
 

@@ -25,7 +25,7 @@ import torch
 
 from . import _lib
 from .ops import HEAD_DIM, _ptr, _require_cuda_fp16, _scratch_args, _stream
-from .step_ops import _batch, _check, _rows, _weight, rope_args
+from .step_ops import PACK_ROPE, _batch, _check, _rows, _weight, rope_args
 
 MIN_PAGE, MAX_PAGE = 64, 4096
 
@@ -299,7 +299,7 @@ def prefill_varlen_paged(query: torch.Tensor, key: torch.Tensor, value: torch.Te
 
 
 def rms_qkv_rope_append_paged(x: torch.Tensor, norm_w: torch.Tensor, eps: float,
-                              w_qkv: torch.Tensor, bias: torch.Tensor | None,
+                              w_qkv, bias: torch.Tensor | None,
                               cos: torch.Tensor | None, sin: torch.Tensor | None,
                               k_pool: torch.Tensor, v_pool: torch.Tensor,
                               block_table: torch.Tensor, slots: torch.Tensor,
@@ -317,7 +317,7 @@ def rms_qkv_rope_append_paged(x: torch.Tensor, norm_w: torch.Tensor, eps: float,
     kvh = k_pool.shape[1]
     hidden = norm_w.shape[0]
     _check("norm_w", norm_w)
-    _weight("w_qkv", w_qkv, (qh + 2 * kvh) * HEAD_DIM, hidden)
+    w_ptr, w_layout = _weight("w_qkv", w_qkv, (qh + 2 * kvh) * HEAD_DIM, hidden, PACK_ROPE)
     if bias is not None:
         _check("bias", bias)
         if tuple(bias.shape) != ((qh + 2 * kvh) * HEAD_DIM,) or not bias.is_contiguous():
@@ -339,7 +339,7 @@ def rms_qkv_rope_append_paged(x: torch.Tensor, norm_w: torch.Tensor, eps: float,
         hidden_out = None
     rc = _lib.load().qf_rms_qkv_rope_append_paged(
         x.data_ptr(), x_sb, _ptr(token), _ptr(hidden_out), ho_sb,
-        norm_w.data_ptr(), float(eps), w_qkv.data_ptr(), _ptr(bias), *rope, *pool, *slot,
+        norm_w.data_ptr(), float(eps), w_ptr, w_layout, _ptr(bias), *rope, *pool, *slot,
         q_out.data_ptr(), q_out.stride(0), q_out.stride(1),
         b, hidden, qh, kvh, HEAD_DIM, _stream(x.device))
     _lib.check(rc, "qf_rms_qkv_rope_append_paged")

@@ -32,6 +32,39 @@ HEAD_DIM = 64
 # lm_head blocks: four per CU on the 256-CU part.
 LM_BLOCKS = 1024
 
+# Weight layouts and packing row maps (include/qf_step.h).
+W_ROWS, W_TILES = 0, 1
+PACK_PLAIN, PACK_SWIGLU, PACK_ROPE = 0, 1, 2
+
+
+class Tiles:
+    """A projection weight packed into matrix-core tiles by ``pack_weight``.
+
+    ``data`` holds the same N*K fp16 values as the (N, K) weight in tile order;
+    ``layout`` is the row map it was packed with.  The step entry points take
+    it in place of the row-major weight and run their MFMA kernels."""
+
+    def __init__(self, data: torch.Tensor, n: int, k: int, layout: int):
+        self.data, self.n, self.k, self.layout = data, n, k, layout
+
+    @property
+    def shape(self):
+        return (self.n, self.k)
+
+
+def pack_weight(w: torch.Tensor, layout: int = PACK_PLAIN) -> Tiles:
+    """Repack a (N, K) fp16 weight (torch Linear layout) into MFMA tiles on its
+    device (one launch; a load-time step with no counterpart in the reference)."""
+    _check("w", w)
+    if w.dim() != 2 or w.stride(1) != 1:
+        raise ValueError("w must be 2-D with unit inner stride")
+    n, k = w.shape
+    out = torch.empty(n * k, device=w.device, dtype=torch.float16)
+    rc = _lib.load().qf_pack_weight(w.data_ptr(), w.stride(0), out.data_ptr(), n, k, layout,
+                                    _stream(w.device))
+    _lib.check(rc, "qf_pack_weight")
+    return Tiles(out, n, k, layout)
+
 
 def _check(name: str, t: torch.Tensor, dtype=torch.float16) -> None:
     if not isinstance(t, torch.Tensor):
@@ -51,10 +84,21 @@ def _rows(name: str, t: torch.Tensor, batch: int, width: int) -> int:
     return t.stride(0)
 
 
-def _weight(name: str, w: torch.Tensor, out_f: int, in_f: int) -> None:
+def _weight(name: str, w, out_f: int, in_f: int, pack: int | None = None):
+    """(pointer, w_layout) of a row-major weight or of its ``Tiles``; ``pack``
+    is the row map an entry point's MFMA kernel expects (None: rows only)."""
+    if isinstance(w, Tiles):
+        if pack is None:
+            raise TypeError(f"{name}: this entry point takes row-major weights only")
+        if w.layout != pack or (w.n, w.k) != (out_f, in_f):
+            raise ValueError(f"{name}: tiles must be ({out_f}, {in_f}) packed with row map {pack} "
+                             f"(got ({w.n}, {w.k}) map {w.layout})")
+        _check(name, w.data)
+        return w.data.data_ptr(), W_TILES
     _check(name, w)
     if tuple(w.shape) != (out_f, in_f) or not w.is_contiguous():
         raise ValueError(f"{name} must be contiguous ({out_f}, {in_f}) (got {tuple(w.shape)})")
+    return w.data_ptr(), W_ROWS
 
 
 def _batch(b: int) -> None:
@@ -85,7 +129,7 @@ def rope_args(cos, sin, positions, batch: int):
     return cos.data_ptr(), sin.data_ptr(), cs_sb, None, None
 
 
-def rms_qkv_rope_append(x: torch.Tensor, norm_w: torch.Tensor, eps: float, w_qkv: torch.Tensor,
+def rms_qkv_rope_append(x: torch.Tensor, norm_w: torch.Tensor, eps: float, w_qkv,
                         bias: torch.Tensor | None, cos: torch.Tensor | None,
                         sin: torch.Tensor | None, key_cache: torch.Tensor,
                         value_cache: torch.Tensor, write_index: torch.Tensor,
@@ -98,6 +142,8 @@ def rms_qkv_rope_append(x: torch.Tensor, norm_w: torch.Tensor, eps: float, w_qkv
     (and copied to ``hidden_out`` when given).  RoPE from ``cos``/``sin``
     (B, 64) fp16 tables, or from ``positions = (pos, inv_freq)`` (the kernel
     forms the identical tables; cos/sin then None).  ``q_out``: (B, QH, 64).
+    ``w_qkv``: the ((QH + 2 KVH) * 64, hidden) weight, or its ``Tiles`` packed
+    with PACK_ROPE (matrix-core kernel).
     """
     b, kvh, cap, d = key_cache.shape
     _batch(b)
@@ -113,7 +159,7 @@ def rms_qkv_rope_append(x: torch.Tensor, norm_w: torch.Tensor, eps: float, w_qkv
     qh = q_out.shape[1]
     hidden = norm_w.shape[0]
     _check("norm_w", norm_w)
-    _weight("w_qkv", w_qkv, (qh + 2 * kvh) * d, hidden)
+    w_ptr, w_layout = _weight("w_qkv", w_qkv, (qh + 2 * kvh) * d, hidden, PACK_ROPE)
     if bias is not None:
         _check("bias", bias)
         if tuple(bias.shape) != ((qh + 2 * kvh) * d,) or not bias.is_contiguous():
@@ -136,7 +182,7 @@ def rms_qkv_rope_append(x: torch.Tensor, norm_w: torch.Tensor, eps: float, w_qkv
     lib = _lib.load()
     rc = lib.qf_rms_qkv_rope_append(
         x.data_ptr(), x_sb, _ptr(token), _ptr(hidden_out), ho_sb,
-        norm_w.data_ptr(), float(eps), w_qkv.data_ptr(), _ptr(bias), *rope,
+        norm_w.data_ptr(), float(eps), w_ptr, w_layout, _ptr(bias), *rope,
         key_cache.data_ptr(), *key_cache.stride()[:3],
         value_cache.data_ptr(), *value_cache.stride()[:3],
         write_index.data_ptr(), q_out.data_ptr(), q_out.stride(0), q_out.stride(1),
@@ -182,18 +228,21 @@ def attn_merge_o_proj(flash, w_o: torch.Tensor, hidden: torch.Tensor) -> None:
     _lib.check(rc, "qf_attn_merge_o_proj")
 
 
-def rms_gate_up_swiglu(x: torch.Tensor, norm_w: torch.Tensor, eps: float, w_gate_up: torch.Tensor,
+def rms_gate_up_swiglu(x: torch.Tensor, norm_w: torch.Tensor, eps: float, w_gate_up,
                        h_out: torch.Tensor) -> None:
-    """h_out <- fp16(fp16(silu(g)) * u), [g | u] = rms_norm(x) @ w_gate_up^T."""
+    """h_out <- fp16(fp16(silu(g)) * u), [g | u] = rms_norm(x) @ w_gate_up^T.
+
+    ``w_gate_up``: the (2I, hidden) weight, or its ``Tiles`` packed with
+    PACK_SWIGLU (matrix-core kernel)."""
     b, hidden = x.shape
     _batch(b)
     inter = w_gate_up.shape[0] // 2
     x_sb = _rows("x", x, b, hidden)
     _check("norm_w", norm_w)
-    _weight("w_gate_up", w_gate_up, 2 * inter, hidden)
+    w_ptr, w_layout = _weight("w_gate_up", w_gate_up, 2 * inter, hidden, PACK_SWIGLU)
     ho_sb = _rows("h_out", h_out, b, inter)
     rc = _lib.load().qf_rms_gate_up_swiglu(x.data_ptr(), x_sb, norm_w.data_ptr(), float(eps),
-                                           w_gate_up.data_ptr(), h_out.data_ptr(), ho_sb,
+                                           w_ptr, w_layout, h_out.data_ptr(), ho_sb,
                                            b, hidden, inter, _stream(x.device))
     _lib.check(rc, "qf_rms_gate_up_swiglu")
 

@@ -115,14 +115,18 @@ def test_step_kernels_reject_bad_arguments():
     assert lib.qf_gemv_residual(16, 896, 16, 16, 896, 1, 8200, 896, None) == -2
     assert lib.qf_gemv_residual(None, 896, 16, 16, 896, 1, 896, 896, None) == -1
     assert lib.qf_gemv_residual(18, 896, 16, 16, 896, 1, 896, 896, None) == -1  # misaligned
-    assert lib.qf_rms_gate_up_swiglu(16, 896, 16, 1e-6, 16, 16, 4864, 1, 2048, 4864, None) == -2
-    assert lib.qf_rms_gate_up_swiglu(16, 896, None, 1e-6, 16, 16, 4864, 1, 896, 4864, None) == -1
+    assert lib.qf_rms_gate_up_swiglu(16, 896, 16, 1e-6, 16, 0, 16, 4864, 1, 2048, 4864, None) == -2
+    assert lib.qf_rms_gate_up_swiglu(16, 896, None, 1e-6, 16, 0, 16, 4864, 1, 896, 4864, None) == -1
+    assert lib.qf_rms_gate_up_swiglu(16, 896, 16, 1e-6, 16, 7, 16, 4864, 1, 896, 4864, None) == -1
+    # tiles need hidden % 32 == 0 and I % 8 == 0
+    assert lib.qf_rms_gate_up_swiglu(16, 888, 16, 1e-6, 16, 1, 16, 4864, 1, 888, 4864, None) == -2
+    assert lib.qf_rms_gate_up_swiglu(16, 896, 16, 1e-6, 16, 1, 16, 4860, 1, 896, 4860, None) == -2
     assert lib.qf_rms_lm_head(16, 896, 16, 1e-6, 16, 16, 100, 16, 0, 1, 896, 100, None) == -1
     assert lib.qf_rms_lm_head(16, 896, 16, 1e-6, 16, 16, 100, 16, 8, 0, 896, 100, None) == -2
     assert lib.qf_argmax_step(16, 8, 1, 16, 16, 4, 4, None, None, None, None) == -1  # rows w/o step
     assert lib.qf_argmax_step(16, 8, 9, 16, None, 0, 0, None, None, None, None) == -2
-    def qkv(cos=16, sin=16, pos=None, inv=None, kc=16, D=64):
-        return lib.qf_rms_qkv_rope_append(16, 896, None, None, 0, 16, 1e-6, 16, None, cos, sin, 64,
+    def qkv(cos=16, sin=16, pos=None, inv=None, kc=16, D=64, lay=0):
+        return lib.qf_rms_qkv_rope_append(16, 896, None, None, 0, 16, 1e-6, 16, lay, None, cos, sin, 64,
                                           pos, inv, kc, 0, 0, 0, 16, 0, 0, 0, 16, 16, 0, 0,
                                           1, 896, 14, 2, D, 64, None)
 
@@ -131,6 +135,7 @@ def test_step_kernels_reject_bad_arguments():
     assert qkv(pos=16, inv=16) == -1             # tables and positions together
     assert qkv(cos=None, sin=None) == -1         # neither RoPE source
     assert qkv(cos=None, sin=None, pos=16) == -1  # positions without inv_freq
+    assert qkv(lay=2) == -1                      # unknown weight layout
 
 
 def test_prefill_workspace_plan():
@@ -202,7 +207,7 @@ def test_paged_entry_points_reject_bad_arguments():
     assert prefill(start=256, max_seqlen=8) == -1  # past the row's 256 slots
 
     def qkv(page=64, slots=16, B=1):
-        return lib.qf_rms_qkv_rope_append_paged(16, 896, None, None, 0, 16, 1e-6, 16, None,
+        return lib.qf_rms_qkv_rope_append_paged(16, 896, None, None, 0, 16, 1e-6, 16, 0, None,
                                                 16, 16, 64, None, None, 16, 8192, 4096, 64,
                                                 16, 8192, 4096, 64, 16, 4, 4, 8, page,
                                                 slots, 1, 16, 896, 64, B, 896, 14, 2, 64, None)
@@ -210,3 +215,14 @@ def test_paged_entry_points_reject_bad_arguments():
     assert qkv(page=100) == -2
     assert qkv(B=5) == -2
     assert qkv(slots=None) == -1
+
+
+def test_pack_weight_rejects_bad_arguments():
+    lib = _lib.load()
+    assert lib.qf_pack_weight(16, 896, 16, 1152, 896, 3, None) == -1     # unknown row map
+    assert lib.qf_pack_weight(16, 896, 16, 1150, 896, 0, None) == -2     # N % 16
+    assert lib.qf_pack_weight(16, 888, 16, 1152, 888, 0, None) == -2     # K % 32
+    assert lib.qf_pack_weight(16, 896, 16, 1136, 896, 2, None) == -2     # ROPE needs N % 64
+    assert lib.qf_pack_weight(None, 896, 16, 1152, 896, 0, None) == -1
+    assert lib.qf_pack_weight(16, 800, 16, 1152, 896, 0, None) == -1     # row stride < K
+    assert lib.qf_pack_weight(18, 896, 16, 1152, 896, 0, None) == -1     # misaligned

@@ -209,8 +209,9 @@ def test_prefill_varlen_paged_at_offset_without_rope(dev):
     assert torch.equal(oracle.pages_to_dense(vp.cpu(), table, full, ppr * page), dense_v)
 
 
+@pytest.mark.parametrize("tiles", [False, True])
 @pytest.mark.parametrize("batch", [1, 4])
-def test_rms_qkv_rope_append_paged_matches_dense(dev, batch):
+def test_rms_qkv_rope_append_paged_matches_dense(dev, batch, tiles):
     gen = torch.Generator().manual_seed(40 + batch)
     hidden, width = 896, (QH + 2 * KVH) * D
     x = torch.randn(batch, hidden, generator=gen).half()
@@ -226,8 +227,9 @@ def test_rms_qkv_rope_append_paged_matches_dense(dev, batch):
     vp0 = torch.randn(n_pages, KVH, page, D, generator=gen).half()
     kp, vp = kp0.to(dev), vp0.to(dev)
     q_out = torch.zeros(batch, QH, D, device=dev, dtype=torch.float16)
-    print(f"[paged qkv] B={batch}", flush=True)
-    paged.rms_qkv_rope_append_paged(x.to(dev), nw.to(dev), 1e-6, w.to(dev), bias.to(dev),
+    print(f"[paged qkv] B={batch} tiles={tiles}", flush=True)
+    wp = step_ops.pack_weight(w.to(dev), step_ops.PACK_ROPE) if tiles else w.to(dev)
+    paged.rms_qkv_rope_append_paged(x.to(dev), nw.to(dev), 1e-6, wp, bias.to(dev),
                                     cos.to(dev), sin.to(dev), kp, vp, table.to(dev),
                                     slots.to(dev), q_out)
     # Dense twin: each row written at its own slot of a dense cache, one row at a time.
@@ -235,7 +237,7 @@ def test_rms_qkv_rope_append_paged_matches_dense(dev, batch):
     vc = torch.zeros_like(kc)
     q_ref = torch.zeros_like(q_out)
     for r in range(batch):
-        step_ops.rms_qkv_rope_append(x[r:r + 1].to(dev), nw.to(dev), 1e-6, w.to(dev), bias.to(dev),
+        step_ops.rms_qkv_rope_append(x[r:r + 1].to(dev), nw.to(dev), 1e-6, wp, bias.to(dev),
                                      cos[r:r + 1].to(dev), sin[r:r + 1].to(dev), kc[r:r + 1],
                                      vc[r:r + 1], torch.tensor([int(slots[r])], device=dev),
                                      q_ref[r:r + 1])

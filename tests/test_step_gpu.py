@@ -48,9 +48,10 @@ def _tables(b, start, dev):
     return cos, sin, cos.to(dev), sin.to(dev)
 
 
+@pytest.mark.parametrize("tiles", [False, True])
 @pytest.mark.parametrize("batch", [1, 2, 3, 4])
 @pytest.mark.parametrize("integer", [True, False])
-def test_rms_qkv_rope_append(dev, batch, integer):
+def test_rms_qkv_rope_append(dev, batch, integer, tiles):
     gen = torch.Generator().manual_seed(10 + batch)
     width = (QH + 2 * KVH) * D
     if integer:
@@ -69,8 +70,9 @@ def test_rms_qkv_rope_append(dev, batch, integer):
     vc0 = _rand(batch, KVH, cap, D, gen=gen)
     kc, vc = kc0.to(dev), vc0.to(dev)
     q_out = torch.zeros(batch, QH, D, device=dev, dtype=torch.float16)
-    print(f"[qkv] B={batch} integer={integer}", flush=True)
-    step_ops.rms_qkv_rope_append(x.to(dev), nw.to(dev), EPS, w.to(dev), bias.to(dev), cos_d, sin_d,
+    print(f"[qkv] B={batch} integer={integer} tiles={tiles}", flush=True)
+    wd = step_ops.pack_weight(w.to(dev), step_ops.PACK_ROPE) if tiles else w.to(dev)
+    step_ops.rms_qkv_rope_append(x.to(dev), nw.to(dev), EPS, wd, bias.to(dev), cos_d, sin_d,
                                  kc, vc, torch.tensor([slot], device=dev), q_out)
     torch.cuda.synchronize()
     q, k, v = ost.qkv_rope16(x, nw, EPS, w, bias, cos, sin, QH, KVH, D)
@@ -90,7 +92,8 @@ def test_rms_qkv_rope_append(dev, batch, integer):
         assert torch.equal(vc.cpu()[:, :, other], vc0[:, :, other])
 
 
-def test_rms_qkv_gathers_embedding_rows_and_skips_out_of_range_slot(dev):
+@pytest.mark.parametrize("tiles", [False, True])
+def test_rms_qkv_gathers_embedding_rows_and_skips_out_of_range_slot(dev, tiles):
     gen = torch.Generator().manual_seed(3)
     batch, vocab = 3, 50
     width = (QH + 2 * KVH) * D
@@ -104,7 +107,8 @@ def test_rms_qkv_gathers_embedding_rows_and_skips_out_of_range_slot(dev):
     vc = torch.zeros_like(kc)
     q_out = torch.zeros(batch, QH, D, device=dev, dtype=torch.float16)
     hidden = torch.zeros(batch, HIDDEN, device=dev, dtype=torch.float16)
-    step_ops.rms_qkv_rope_append(embed.to(dev), nw.to(dev), EPS, w.to(dev), None, cos_d, sin_d,
+    wd = step_ops.pack_weight(w.to(dev), step_ops.PACK_ROPE) if tiles else w.to(dev)
+    step_ops.rms_qkv_rope_append(embed.to(dev), nw.to(dev), EPS, wd, None, cos_d, sin_d,
                                  kc, vc, torch.tensor([cap], device=dev), q_out,
                                  token=token.to(dev), hidden_out=hidden)
     torch.cuda.synchronize()
@@ -137,9 +141,10 @@ def test_gemv_residual(dev, batch, k_dim, n, integer):
         assert ok, err
 
 
-@pytest.mark.parametrize("batch", [1, 2, 4])
+@pytest.mark.parametrize("tiles", [False, True])
+@pytest.mark.parametrize("batch", [1, 2, 3, 4])
 @pytest.mark.parametrize("integer", [True, False])
-def test_rms_gate_up_swiglu(dev, batch, integer):
+def test_rms_gate_up_swiglu(dev, batch, integer, tiles):
     gen = torch.Generator().manual_seed(20 + batch)
     if integer:
         x = _int_rows(batch, HIDDEN, gen)
@@ -150,8 +155,9 @@ def test_rms_gate_up_swiglu(dev, batch, integer):
         nw = (torch.rand(HIDDEN, generator=gen) + 0.5).to(torch.float16)
         w = _rand(2 * INTER, HIDDEN, gen=gen, std=0.02)
     h = torch.zeros(batch, INTER, device=dev, dtype=torch.float16)
-    print(f"[gate_up] B={batch} integer={integer}", flush=True)
-    step_ops.rms_gate_up_swiglu(x.to(dev), nw.to(dev), EPS, w.to(dev), h)
+    print(f"[gate_up] B={batch} integer={integer} tiles={tiles}", flush=True)
+    wd = step_ops.pack_weight(w.to(dev), step_ops.PACK_SWIGLU) if tiles else w.to(dev)
+    step_ops.rms_gate_up_swiglu(x.to(dev), nw.to(dev), EPS, wd, h)
     torch.cuda.synchronize()
     ref = ost.swiglu16(x, nw, EPS, w)
     # silu's exp may differ in the last fp32 bit between the device and the CPU
@@ -245,8 +251,9 @@ def test_attn_merge_o_proj(dev, batch, splits):
     assert ok, err
 
 
+@pytest.mark.parametrize("tiles", [False, True])
 @pytest.mark.parametrize("batch", [1, 3, 4])
-def test_rms_qkv_rope_positions_mode_equals_table_mode(dev, batch):
+def test_rms_qkv_rope_positions_mode_equals_table_mode(dev, batch, tiles):
     """RoPE angles formed in the kernel from (pos, inv_freq) give exactly the
     outputs of the torch-built fp16 tables (SE:910-915), including far
     positions and a negative one."""
@@ -262,6 +269,8 @@ def test_rms_qkv_rope_positions_mode_equals_table_mode(dev, batch):
     inv = make_inv(D, 1e6, dev)
     cos, sin = cos_sin(pos, inv)
     cap, slot = 64, 9
+    if tiles:
+        w = step_ops.pack_weight(w, step_ops.PACK_ROPE)
     outs = []
     for mode in ("table", "positions"):
         kc = torch.zeros(batch, KVH, cap, D, device=dev, dtype=torch.float16)
@@ -278,3 +287,28 @@ def test_rms_qkv_rope_positions_mode_equals_table_mode(dev, batch):
     torch.cuda.synchronize()
     for a, b in zip(*outs):
         assert torch.equal(a.cpu(), b.cpu())
+
+
+@pytest.mark.parametrize("layout", [0, 1, 2])
+def test_pack_weight_tile_order(dev, layout):
+    """Every 16-byte chunk of a packed weight is the row-major chunk the tile
+    formula names (row maps plain, SwiGLU pairs, rotate-half pairs)."""
+    n, k = 256, 96
+    w = torch.arange(n * k, dtype=torch.float32).remainder(2039).to(torch.float16).view(n, k)
+    tiles = step_ops.pack_weight(w.to(dev), layout)
+    torch.cuda.synchronize()
+    got = tiles.data.cpu().view(n // 16, k // 32, 64, 8)
+    for rb in range(n // 16):
+        for r in range(16):
+            g, i = r >> 2, r & 3
+            if layout == 1:
+                j = 8 * rb + 2 * g + (i & 1)
+                row = n // 2 + j if i & 2 else j
+            elif layout == 2:
+                row = 64 * (rb >> 2) + 8 * (rb & 3) + 2 * g + (i & 1) + (32 if i & 2 else 0)
+            else:
+                row = 16 * rb + r
+            for kb in range(k // 32):
+                for q in range(4):
+                    want = w[row, 32 * kb + 8 * q: 32 * kb + 8 * q + 8]
+                    assert torch.equal(got[rb, kb, 16 * q + r], want), (rb, r, kb, q)
