@@ -117,19 +117,20 @@ def bench_ragged_decode(steps, warmup, dev):
     step_bytes = sum(c.valid_bytes for c in layers)
     fused = len(flash) > 4
 
-    # The dominant kernel alone: the split launch (qf_decode_split) over the
-    # same 24 layers, then the combine launch alone (unfused shape only).
-    def split_fn(cs):
-        def run():
-            for i, c in enumerate(cs):
-                ops.flash_decode_split(c.grouped, c.key_cache, c.value_cache, c.bias, flash[:4],
-                                       kv_last=kv_last[i])
-        return run
-
-    split_graphs = [GraphStep(split_fn(cs)) for cs in sets]
-    ms_split = _time_graphs(split_graphs, steps, warmup)
-    ms_combine = None
+    # The dominant kernel alone.  With the single-launch merge the call is one
+    # kernel, so the full call is that kernel; otherwise the split launch
+    # (qf_decode_split) over the same 24 layers, then the combine alone.
+    ms_split, ms_combine = ms, None
     if not fused:
+        def split_fn(cs):
+            def run():
+                for i, c in enumerate(cs):
+                    ops.flash_decode_split(c.grouped, c.key_cache, c.value_cache, c.bias,
+                                           flash[:4], kv_last=kv_last[i])
+            return run
+
+        split_graphs = [GraphStep(split_fn(cs)) for cs in sets]
+        ms_split = _time_graphs(split_graphs, steps, warmup)
         comb = GraphStep(lambda: [ops.flash_decode_combine(flash[:4]) for _ in layers])
         ms_combine = _time_graphs([comb], steps, warmup)
     return dict(ms_per_step=ms, step_bytes=step_bytes, launches=len(layers), splits=splits,
@@ -381,7 +382,8 @@ def bench_e2e(dev, batches=(1, 4), prefix=1024, new_tokens=128):
 def pmc_sample(dev):
     """A short fixed sequence for ``rocprofv3 --pmc`` passes (no timing):
     a plain 64 MiB device copy (calibrates FETCH_SIZE / WRITE_SIZE against a
-    known byte count), then one config-2 step of split and combine launches."""
+    known byte count), then one config-2 step: 24 decode-attention calls with
+    the headline's split count and merge (single launch per call)."""
     import torch
 
     from qwenforge_amd import ops, workloads
@@ -393,12 +395,11 @@ def pmc_sample(dev):
     torch.cuda.synchronize()
     layers = [c.to(dev) for c in workloads.decode_ragged_layers(24, 4, seed=0)]
     cap_max = max(c.key_cache.shape[2] for c in layers)
-    flash = ops.make_flash_scratch(4, 2, 7, cap_max, dev, splits=ops.choose_splits(4, 2, cap_max),
-                                   fused=False)
+    flash = ops.make_flash_scratch(4, 2, 7, cap_max, dev, splits=ops.choose_splits(4, 2, cap_max))
     for c in layers:
         kv_last = torch.tensor([n - 1 for n in c.lengths], dtype=torch.int64, device=dev)
-        ops.flash_decode_split(c.grouped, c.key_cache, c.value_cache, c.bias, flash, kv_last=kv_last)
-        ops.flash_decode_combine(flash)
+        ops.flash_decode_attention(c.grouped, c.key_cache, c.value_cache, c.bias, flash,
+                                   kv_last=kv_last)
     torch.cuda.synchronize()
     print(json.dumps({"pmc_sample": "done", "copy_bytes": 2 * src.numel() * 2,
                       "split_launches": len(layers),
@@ -406,7 +407,8 @@ def pmc_sample(dev):
 
 
 def _traffic():
-    """HBM bytes per split launch measured with rocprofv3 counters (see profiles/)."""
+    """HBM bytes per launch of the headline's dominant kernel, measured with
+    rocprofv3 counters (profiles/decode_split_cfg2_traffic.json)."""
     path = os.path.join(ROOT, "profiles", "decode_split_cfg2_traffic.json")
     if not os.path.exists(path):
         return None
@@ -503,7 +505,10 @@ def main():
             "unit": "GB/s",
             "frac": round(split_gbs / HBM_PEAK_GBS, 4),
             "traffic": _traffic(),
-            "kernel": "qf::decode_split_kernel<8, 1, 1, false> (qf_decode_split: 8 waves, vector bias, partial mode, dense cache)",
+            "kernel": ("qf::decode_split_kernel<8, 1, 2, false> (qf_decode_attn: 8 waves, vector bias, "
+                       "single-launch merge, dense cache; the whole call)" if r["fused"] else
+                       "qf::decode_split_kernel<8, 1, 1, false> (qf_decode_split: 8 waves, vector bias, "
+                       "partial mode, dense cache)"),
             "bytes_per_launch": int(launch_bytes),
             "avg_launch_us": round(us_split, 3),
             "combine_kernel_avg_us": (None if r["ms_combine"] is None

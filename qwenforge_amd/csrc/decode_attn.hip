@@ -24,14 +24,14 @@
 //             layout and a second kernel merges them (the reference's
 //             two-launch shape);
 //   kFused    it writes the partial with write-through (sc1) stores and takes
-//             a device-scope ticket; the last workgroup of each group of 16
-//             splits merges its group in place into the group's first split,
-//             and the last group merger writes the output and re-arms the
-//             tickets.  Write-through stores plus a wait for their completion
-//             replace an agent-scope release fence, which on this part writes
-//             back the whole L2 per workgroup.
-// Every merge is one pass of independent loads spread over the whole
-// workgroup, so each level costs one dependent memory round trip.
+//             a device-scope ticket; the last workgroup of the (b, h) merges
+//             all S partials (one wave per query), writes the output and
+//             re-arms the ticket.  Write-through stores plus a wait for their
+//             completion replace an agent-scope release fence, which on this
+//             part writes back the whole L2 per workgroup.
+// Every merge is one pass of independent loads (eight partials per lane in
+// flight) followed by register / permlane / LDS reductions, so it costs one
+// dependent memory round trip.
 #include "qf_common.h"
 #include "../../include/qf_attn.h"
 #include "../../include/qf_paged.h"
@@ -42,10 +42,6 @@ constexpr int kD = 64;
 constexpr int kTile = 32;       // keys per wave iteration
 constexpr int kVtStride = 36;   // LDS row stride (halves) of a transposed V tile
 constexpr int kMaxG = 16;
-#ifndef QF_DECODE_GROUP
-#define QF_DECODE_GROUP 16
-#endif
-constexpr int kGroup = QF_DECODE_GROUP;  // splits per first-level merge group
 
 enum Mode { kDirect = 0, kPartial = 1, kFused = 2 };
 
@@ -91,7 +87,12 @@ __device__ __forceinline__ float ld(const float* p) {
   return *p;
 }
 
-// Slot range [lo, hi) of split `s` for batch row `b`.
+// Slot range [lo, hi) of split `s` for batch row `b`: the row's valid slots
+// end at upper = kv_last[b] + 1 (clamped to [0, cap]; cap without a bound)
+// and split_len = ceil(upper / S), rounded up to whole 32-key tiles.  (The
+// reference splits the capacity, split_len = ceil(cap / S) at SE:851;
+// splitting the bound keeps every split busy, and reads nothing, past the
+// newest slot.)
 __device__ __forceinline__ void split_range(const DecodeArgs& a, int b, int s, int& lo, int& hi) {
   int upper = a.cap;
   if (a.kv_last != nullptr) {
@@ -104,100 +105,112 @@ __device__ __forceinline__ void split_range(const DecodeArgs& a, int b, int s, i
   hi = lo + split_len < upper ? lo + split_len : upper;
 }
 
-// Log-sum-exp merge of `count` partials of (b, h) = bh at split indices
-// first + j*stride, for queries [q0, q0 + nq).  Work item = (query, 4 output
-// dims); the NT threads of the workgroup split each item's partials among
-// `tpi` threads, each folding its share with independent loads (8 at a
-// time), and the shares are combined through LDS.  `final`: write fp16
-// out = acc / l.  Otherwise write the merged partial in place at split
-// `first` (the thread that writes a slice is the only one that read it in
-// this call, and m/l of split `first` are written after the barrier that
-// follows every read).  Every thread of the workgroup must call this.
-template <int NT, bool kCoherent>
-__device__ void merge_parts(const DecodeArgs& a, int bh, int q0, int nq, int first, int stride,
-                            int count, bool final, float* lds) {
-  const int G = a.G;
-  const int items = nq * 16;
-  const int tpi = NT / items;  // threads per item (>= 1: items <= 256 <= NT)
-  const int tid = threadIdx.x;
-  const int item = tid % items, sub = tid / items;
-  const int q = q0 + item / 16, d4 = item % 16;
-  const int64_t pbase = (int64_t)bh * a.splits;
-  float M = kNegInf, L = 0.f;
-  f32x4 A = {0.f, 0.f, 0.f, 0.f};
-  if (sub < tpi) {
-    for (int j0 = sub; j0 < count; j0 += 8 * tpi) {
-      float mv[8], lv[8];
-      f32x4 av[8];
+// (M, L, A) <- log-sum-exp merge of two partial states (m in natural-log
+// units, -inf for an empty state).
+__device__ __forceinline__ void lse_merge(float& M, float& L, f32x4& A, float M2, float L2,
+                                          f32x4 A2) {
+  const float mn = fmaxf(M, M2);
+  const float safe = (mn == kNegInf) ? 0.f : mn;
+  const float w1 = (M == kNegInf) ? 0.f : fast_exp2((M - safe) * kLog2e);
+  const float w2 = (M2 == kNegInf) ? 0.f : fast_exp2((M2 - safe) * kLog2e);
+  L = L * w1 + L2 * w2;
+  A = A * w1 + A2 * w2;
+  M = mn;
+}
+
+// Merges the states of lanes l and l ^ 16 (kXor32: l ^ 32).  The permlane
+// swaps hand both lanes the pair in the same (lower row, upper row) order, so
+// the two lanes end with bit-identical states.
+template <bool kXor32>
+__device__ __forceinline__ void lse_merge_lanes(float& M, float& L, f32x4& A) {
+  float m0, m1, l0, l1;
+  f32x4 a0, a1;
+  const auto pair = [](float x, float& lo, float& hi) {
+    if (kXor32) xor32_pair(x, lo, hi);
+    else xor16_pair(x, lo, hi);
+  };
+  pair(M, m0, m1);
+  pair(L, l0, l1);
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const int j = j0 + u * tpi;
-        if (j < count) {
-          const int64_t part = pbase + first + (int64_t)j * stride;
-          const float* ap = a.acc + (part * G + q) * kD + 4 * d4;
-          mv[u] = ld<kCoherent>(a.m + part * G + q);
-          lv[u] = ld<kCoherent>(a.l + part * G + q);
-          av[u] = f32x4{ld<kCoherent>(ap), ld<kCoherent>(ap + 1), ld<kCoherent>(ap + 2),
-                        ld<kCoherent>(ap + 3)};
-        } else {
-          mv[u] = kNegInf;
-          lv[u] = 0.f;
-          av[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-      }
-      float mc = mv[0];
-#pragma unroll
-      for (int u = 1; u < 8; ++u) mc = fmaxf(mc, mv[u]);
-      const float mn = fmaxf(M, mc);
-      const float safe = (mn == kNegInf) ? 0.f : mn;
-      const float r = (M == kNegInf) ? 0.f : fast_exp2((M - safe) * kLog2e);
-      L *= r;
-      A *= r;
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        const float w = (mv[u] == kNegInf) ? 0.f : fast_exp2((mv[u] - safe) * kLog2e);
-        L += w * lv[u];
-        A += w * av[u];
-      }
-      M = mn;
-    }
+  for (int c = 0; c < 4; ++c) {
+    float lo, hi;
+    pair(A[c], lo, hi);
+    a0[c] = lo;
+    a1[c] = hi;
   }
-  // Combine the tpi shares of every item: lds[(sub * items + item) * 6 + ...].
-  if (sub < tpi) {
-    float* e = lds + (sub * items + item) * 6;
-    e[0] = M; e[1] = L; e[2] = A[0]; e[3] = A[1]; e[4] = A[2]; e[5] = A[3];
-  }
-  __syncthreads();
-  if (tid < items) {
-    float Mt = kNegInf;
-    for (int s2 = 0; s2 < tpi; ++s2) Mt = fmaxf(Mt, lds[(s2 * items + item) * 6]);
-    const float safe = (Mt == kNegInf) ? 0.f : Mt;
-    float Lt = 0.f;
-    f32x4 At = {0.f, 0.f, 0.f, 0.f};
-    for (int s2 = 0; s2 < tpi; ++s2) {
-      const float* e = lds + (s2 * items + item) * 6;
-      const float w = (e[0] == kNegInf) ? 0.f : fast_exp2((e[0] - safe) * kLog2e);
-      Lt += w * e[1];
-      At += w * f32x4{e[2], e[3], e[4], e[5]};
-    }
-    if (final) {
-      const float inv = 1.f / Lt;
-      const int b = bh / a.KVH, h = bh % a.KVH;
-      f16x4 o;
+  lse_merge(m0, l0, a0, m1, l1, a1);
+  M = m0;
+  L = l0;
+  A = a0;
+}
+
+// Cache policy of partial-scratch accesses in the single-launch merge: sc1,
+// the bits the gfx950 memory model gives relaxed agent-scope atomic loads and
+// stores (write-through / L2-bypassing), on 16-byte buffer accesses.
+constexpr int kSc1 = 16;
+
+// Buffer resource over `bytes` bytes at `base` (loads past the end return 0).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
+                                           (int)(bytes < 0x7fffffff ? bytes : 0x7fffffff),
+                                           0x00020000);
+}
+
+// Folds partials j = j0, j0 + step, ... (< S) of (b, h) = bh, query q, dims
+// 4*d4 .. +3 into the running state (M, L, A), eight partials per batch with
+// every load of a batch issued before the first use.  The loads are buffer
+// loads bounded to this (b, h)'s partials: slots past S read 0 and get weight
+// 0.  kCoherent: sc1 loads, for partials written by other workgroups of the
+// same launch with sc1 stores.
+template <bool kCoherent>
+__device__ __forceinline__ void fold_partials(const DecodeArgs& a, int bh, int q, int d4, int j0,
+                                              int step, float& M, float& L, f32x4& A) {
+  const int G = a.G, S = a.splits;
+  const int64_t pbase = (int64_t)bh * S;
+  constexpr int aux = kCoherent ? kSc1 : 0;
+  const __amdgpu_buffer_rsrc_t ra = rsrc(a.acc + pbase * G * kD, (int64_t)S * G * kD * 4);
+  const __amdgpu_buffer_rsrc_t rm = rsrc(a.m + pbase * G, (int64_t)S * G * 4);
+  const __amdgpu_buffer_rsrc_t rl = rsrc(a.l + pbase * G, (int64_t)S * G * 4);
+  for (; j0 < S; j0 += 8 * step) {
+    float mv[8], lv[8];
+    f32x4 av[8];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) o[c] = (f16)(At[c] * inv);
-      *reinterpret_cast<f16x4*>(a.out + b * a.o_sb + h * a.o_sh + q * a.o_sg + 4 * d4) = o;
-    } else {
-      const int64_t part = pbase + first;
-      float* ap = a.acc + (part * G + q) * kD + 4 * d4;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) st<kCoherent>(ap + c, At[c]);
-      if (d4 == 0) {
-        st<kCoherent>(a.m + part * G + q, Mt);
-        st<kCoherent>(a.l + part * G + q, Lt);
-      }
+    for (int u = 0; u < 8; ++u) {
+      const int j = j0 + step * u;
+      const int row = j * G + q;
+      mv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rm, row * 4, 0, aux));
+      lv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, row * 4, 0, aux));
+      av[u] = __builtin_bit_cast(
+          f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, (row * kD + 4 * d4) * 4, 0, aux));
     }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (j0 + step * u >= S) mv[u] = kNegInf;
+    float mc = mv[0];
+#pragma unroll
+    for (int u = 1; u < 8; ++u) mc = fmaxf(mc, mv[u]);
+    const float mn = fmaxf(M, mc);
+    const float safe = (mn == kNegInf) ? 0.f : mn;
+    const float r = (M == kNegInf) ? 0.f : fast_exp2((M - safe) * kLog2e);
+    L *= r;
+    A *= r;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const float wu = (mv[u] == kNegInf) ? 0.f : fast_exp2((mv[u] - safe) * kLog2e);
+      L += wu * lv[u];
+      A += wu * av[u];
+    }
+    M = mn;
   }
+}
+
+// fp16 out[b, h, q, 4*d4 .. +3] = A / L.
+__device__ __forceinline__ void store_out(const DecodeArgs& a, int bh, int q, int d4, float L,
+                                          f32x4 A) {
+  const float inv = 1.f / L;
+  const int b = bh / a.KVH, h = bh % a.KVH;
+  const f16x4 o = {(f16)(A[0] * inv), (f16)(A[1] * inv), (f16)(A[2] * inv), (f16)(A[3] * inv)};
+  *reinterpret_cast<f16x4*>(a.out + b * a.o_sb + h * a.o_sh + q * a.o_sg + 4 * d4) = o;
 }
 
 enum Bias { kNoBias = 0, kBiasVec = 1, kBiasScalar = 2 };
@@ -261,10 +274,8 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
   // LDS: per-wave transposed V tiles during the sweep, reused for the
   // cross-wave merge and the split merges afterwards.
   constexpr int kVtBytes = NW * kD * kVtStride * 2;
-  constexpr int kWaveMergeBytes = NW * kMaxG * (kD + 1) * 4;
-  constexpr int kSplitMergeBytes = NT * 6 * 4;
-  constexpr int kA = kVtBytes > kWaveMergeBytes ? kVtBytes : kWaveMergeBytes;
-  constexpr int kLdsBytes = kA > kSplitMergeBytes ? kA : kSplitMergeBytes;
+  constexpr int kWaveMergeBytes = NW * 4 * 64 * 16;
+  constexpr int kLdsBytes = kVtBytes > kWaveMergeBytes ? kVtBytes : kWaveMergeBytes;
   __shared__ __attribute__((aligned(16))) unsigned char lds_raw[kLdsBytes];
   __shared__ float sm_ml[2][NW][kMaxG];
   __shared__ int sh_last;
@@ -308,7 +319,6 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
   const f16* vb = a.v + b * a.v_sb + h * a.v_sh;
   const f16* biasb = kHasBias ? a.bias + b * a.bias_sb : nullptr;
   f16(*vt)[kVtStride] = reinterpret_cast<f16(*)[kVtStride]>(lds_raw + w * kD * kVtStride * 2);
-  const int last = hi - 1;
 
   // Paged caches: lane j holds the physical page of this wave's tile
   // win + j (tile i of the wave starts at lo + (w + i*NW) * kTile and lies in
@@ -316,9 +326,9 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
   // kTile boundaries); one load per 64 tiles of the wave.  The tile's base
   // pointers are then shifted so that logical slot numbers index them.
   int pid = 0;
-  const auto load_pids = [&](int win) {
+  const auto load_pids = [&](int win, int clamp) {
     int t = lo + (w + (win + lane) * NW) * kTile;
-    t = t < last ? t : last;
+    t = t < clamp ? t : clamp;
     pid = page_of(a, b, t > 0 ? t : 0);
   };
   const auto tile_base = [&](int i, int t0, const f16*& kt, const f16*& vtb) {
@@ -333,10 +343,11 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     vtb = a.v + (int64_t)page * a.v_sp + h * a.v_sh - first * a.v_sn;
   };
 
+  const int last = hi - 1;
   int t0 = lo + w * kTile;
   Tile cur, nxt;
   const f16 *kt_, *vt_;
-  if (kPaged && t0 < hi) load_pids(0);
+  if (kPaged && t0 < hi) load_pids(0, last);
   if (t0 < hi) {
     tile_base(0, t0, kt_, vt_);
     load_tile<kBias>(cur, kt_, vt_, biasb, a.k_sn, a.v_sn, t0, last, a.cap, lane);
@@ -344,7 +355,7 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
   for (int i = 0; t0 < hi; t0 += NW * kTile, ++i) {
     const int tn = t0 + NW * kTile;
     if (tn < hi) {
-      if (kPaged && ((i + 1) & 63) == 0) load_pids(i + 1);
+      if (kPaged && ((i + 1) & 63) == 0) load_pids(i + 1, last);
       tile_base(i + 1, tn, kt_, vt_);
       load_tile<kBias>(nxt, kt_, vt_, biasb, a.k_sn, a.v_sn, tn, last, a.cap, lane);
     }
@@ -412,84 +423,116 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
 
   l_run = col_sum(l_run);
 
-  // Cross-wave merge through LDS (the V tiles are dead now).
-  __syncthreads();
-  float* sm_o = reinterpret_cast<float*>(lds_raw);  // [NW][16][kD + 1]
-  constexpr int kOStride = kD + 1;
+  // Cross-wave merge.  A wave's softmax state is replicated over the four
+  // lanes of each query column.  The waves exchange (m, l) per column; each
+  // wave then scales its accumulator by exp2(m_w - M) and writes it to LDS as
+  // 16-byte rows [w][t][lane]; wave w' < min(NW, 4) sums the NW rows of its
+  // 16-dim slices t = w', w' + NW, ... and stores them from the MFMA layout
+  // (lane (q, grp) holds dims 16t + 4grp .. +3 of query q).  Two barriers;
+  // each LDS pass is one round of independent accesses.
   if (grp == 0) {
     sm_ml[0][w][col] = m_run;
     sm_ml[1][w][col] = l_run;
   }
+  __syncthreads();  // (m, l) visible; every wave is done with its V tiles
+  float M = kNegInf;
 #pragma unroll
-  for (int t = 0; t < 4; ++t)
+  for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, sm_ml[0][ww][col]);
+  const float safe = (M == kNegInf) ? 0.f : M;
+  float L = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sm_o[(w * kMaxG + col) * kOStride + 16 * t + 4 * grp + i] = o[t][i];
+  for (int ww = 0; ww < NW; ++ww) {
+    const float mw = sm_ml[0][ww][col];
+    L += ((mw == kNegInf) ? 0.f : fast_exp2(mw - safe)) * sm_ml[1][ww][col];
+  }
+  const float wt = (m_run == kNegInf) ? 0.f : fast_exp2(m_run - safe);
+  f32x4* sm_o = reinterpret_cast<f32x4*>(lds_raw);  // [NW][4][64]
+#pragma unroll
+  for (int t = 0; t < 4; ++t) sm_o[(w * 4 + t) * 64 + lane] = o[t] * wt;
   __syncthreads();
 
   const int S = a.splits, G = a.G;
   const int64_t part = (int64_t)bh * S + s;
-  for (int e = tid; e < G * kD; e += NT) {
-    const int q = e / kD, d = e % kD;
-    float mx = kNegInf;
+  for (int t = w; t < 4; t += NW) {
+    f32x4 acc = sm_o[t * 64 + lane];
 #pragma unroll
-    for (int ww = 0; ww < NW; ++ww) mx = fmaxf(mx, sm_ml[0][ww][q]);
-    const float safe = (mx == kNegInf) ? 0.f : mx;
-    float so = 0.f, sl = 0.f;
-#pragma unroll
-    for (int ww = 0; ww < NW; ++ww) {
-      const float mw = sm_ml[0][ww][q];
-      const float wt = (mw == kNegInf) ? 0.f : fast_exp2(mw - safe);
-      so += wt * sm_o[(ww * kMaxG + q) * kOStride + d];
-      sl += wt * sm_ml[1][ww][q];
-    }
-    if (kMode == kDirect) {
-      a.out[b * a.o_sb + h * a.o_sh + q * a.o_sg + d] = (f16)(so / sl);
-    } else {
-      st<kCoh>(a.acc + (part * G + q) * kD + d, so);
-      if (d == 0) {
-        st<kCoh>(a.m + part * G + q, (mx == kNegInf) ? kNegInf : mx * kLn2);
-        st<kCoh>(a.l + part * G + q, sl);
+    for (int ww = 1; ww < NW; ++ww) acc += sm_o[(ww * 4 + t) * 64 + lane];
+    if (col < G) {
+      const int d = 16 * t + 4 * grp;
+      if (kMode == kDirect) {
+        const float inv = 1.f / L;
+        const f16x4 ov = {(f16)(acc[0] * inv), (f16)(acc[1] * inv), (f16)(acc[2] * inv),
+                          (f16)(acc[3] * inv)};
+        *reinterpret_cast<f16x4*>(a.out + b * a.o_sb + h * a.o_sh + col * a.o_sg + d) = ov;
+      } else if (kCoh) {
+        // The resource must be wave-uniform (it lives in SGPRs): one per
+        // split, the lane's query row and dims go in the offset.
+        const __amdgpu_buffer_rsrc_t ra = rsrc(a.acc + part * G * kD, (int64_t)G * kD * 4);
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc), ra,
+                                               (col * kD + d) * 4, 0, kSc1);
+      } else {
+        *reinterpret_cast<f32x4*>(a.acc + (part * G + col) * kD + d) = acc;
       }
     }
   }
+  if (kMode != kDirect && w == 0 && grp == 0 && col < G) {
+    st<kCoh>(a.m + part * G + col, (M == kNegInf) ? kNegInf : M * kLn2);
+    st<kCoh>(a.l + part * G + col, L);
+  }
 
   if (kMode == kFused) {
-    float* lds = reinterpret_cast<float*>(lds_raw);
-    const int ng = (S + kGroup - 1) / kGroup;
-    const int g = s / kGroup;
-    const int gsize = (S - g * kGroup) < kGroup ? (S - g * kGroup) : kGroup;
-    int32_t* tk = a.ticket + (int64_t)bh * (ng + 1);
     // Wait until this workgroup's write-through stores have completed, then
-    // take a ticket; the workgroup that completes a count merges.
+    // take the (b, h) ticket; the workgroup that completes the count merges
+    // all S partials -- wave w takes queries w, w + NW, ...; within a wave
+    // lane (sub = lane / 16, d4 = lane % 16) folds partials j = sub (mod 4)
+    // and the four subs merge through permlane swaps -- then re-arms the
+    // ticket.  The ticket of (b, h) is the first of its ceil(S/16) + 1 slots.
+    int32_t* tk = a.ticket + (int64_t)bh * ((S + 15) / 16 + 1);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
     __syncthreads();
-    if (tid == 0) sh_last = (atomicAdd(tk + g, 1) == gsize - 1);
+    if (tid == 0) sh_last = (atomicAdd(tk, 1) == S - 1);
     __syncthreads();
     if (!sh_last) return;
-    if (ng == 1) {
-      merge_parts<NT, true>(a, bh, 0, G, 0, 1, S, true, lds);
-      if (tid == 0) atomicExch(tk + g, 0);
-      return;
+    for (int q = w; q < G; q += NW) {
+      float Mq = kNegInf, Lq = 0.f;
+      f32x4 Aq = {0.f, 0.f, 0.f, 0.f};
+      fold_partials<true>(a, bh, q, lane & 15, lane >> 4, 4, Mq, Lq, Aq);
+      lse_merge_lanes<false>(Mq, Lq, Aq);
+      lse_merge_lanes<true>(Mq, Lq, Aq);
+      if (lane < 16) store_out(a, bh, q, lane, Lq, Aq);
     }
-    merge_parts<NT, true>(a, bh, 0, G, g * kGroup, 1, gsize, false, lds);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __syncthreads();
-    if (tid == 0) {
-      atomicExch(tk + g, 0);
-      sh_last = (atomicAdd(tk + ng, 1) == ng - 1);
-    }
-    __syncthreads();
-    if (!sh_last) return;
-    merge_parts<NT, true>(a, bh, 0, G, 0, kGroup, ng, true, lds);
-    if (tid == 0) atomicExch(tk + ng, 0);
+    if (tid == 0) atomicExch(tk, 0);
   }
 }
 
-// Second launch of the two-kernel shape: one workgroup per (b, h, query).
+// Second launch of the two-kernel shape: one workgroup of four waves per
+// (b, h, query).  Thread (sub = tid / 16, d4 = tid % 16) folds partials
+// j = sub, sub + 16, ... of dims 4*d4 .. +3, with all loads of a batch of
+// eight issued before use; the 4 subs of a wave merge through permlane swaps
+// (lanes d4 + 16r), the 4 waves through LDS, and wave 0 writes fp16 acc / l.
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
-  __shared__ float lds[256 * 6];
+  __shared__ float red[3][16][6];
   const int bh = blockIdx.x / a.G, q = blockIdx.x % a.G;
-  merge_parts<256, false>(a, bh, q, 1, 0, 1, a.splits, true, lds);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int d4 = lane & 15, sub = tid >> 4;
+  float M = kNegInf, L = 0.f;
+  f32x4 A = {0.f, 0.f, 0.f, 0.f};
+  fold_partials<false>(a, bh, q, d4, sub, 16, M, L, A);
+  lse_merge_lanes<false>(M, L, A);
+  lse_merge_lanes<true>(M, L, A);
+  if (w > 0 && lane < 16) {
+    float* e = red[w - 1][lane];
+    e[0] = M; e[1] = L; e[2] = A[0]; e[3] = A[1]; e[4] = A[2]; e[5] = A[3];
+  }
+  __syncthreads();
+  if (w == 0 && lane < 16) {
+#pragma unroll
+    for (int ww = 0; ww < 3; ++ww) {
+      const float* e = red[ww][lane];
+      lse_merge(M, L, A, e[0], e[1], f32x4{e[2], e[3], e[4], e[5]});
+    }
+    store_out(a, bh, q, d4, L, A);
+  }
 }
 
 template <int NW, int kBias, bool kPaged>
@@ -519,15 +562,20 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // Waves per workgroup (measured on MI355X): sixteen when one workgroup per
 // kv head streams everything, eight up to two workgroups per CU (also for
 // small grids: at B=1 with 8 splits, 8 waves beat 16 by 0.7 us per call), four
-// for large grids.
-static int pick_waves(int splits, int B, int KVH) {
+// for large grids -- and never more waves than the split has 32-key tiles
+// (idle waves only lengthen the cross-wave merge).  The single-launch merge
+// gives each query a wave: NW >= G.
+static int pick_waves(const DecodeArgs& a, int mode) {
 #ifdef QF_DECODE_FORCE_NW
   return QF_DECODE_FORCE_NW;
 #endif
-  const int64_t wgs = (int64_t)splits * B * KVH;
-  if (wgs <= 2) return 16;
-  if (wgs <= 512) return 8;
-  return 4;
+  const int64_t wgs = (int64_t)a.splits * a.B * a.KVH;
+  int nw = wgs <= 2 ? 16 : (wgs <= 512 ? 8 : 4);
+  const int split_len = (a.cap + a.splits - 1) / a.splits;
+  const int tiles = (split_len + kTile - 1) / kTile;
+  const int min_nw = mode == kFused ? a.G : 1;
+  while (nw > 2 && nw / 2 >= tiles && nw / 2 >= min_nw) nw /= 2;
+  return nw;
 }
 
 // Validates the decode arguments and fills DecodeArgs; 0 or a QF_ERR_* code.
@@ -584,10 +632,11 @@ static int make_args(DecodeArgs& a, const void* q, int64_t q_sb, int64_t q_sh, i
 template <bool kPaged>
 static void launch_split_paging(const DecodeArgs& a, int mode, hipStream_t st) {
   const dim3 grid(a.splits, a.B * a.KVH);
-  const int nw = pick_waves(a.splits, a.B, a.KVH);
+  const int nw = pick_waves(a, mode);
   if (nw == 16) launch_nw<16, kPaged>(a, mode, grid, st);
   else if (nw == 8) launch_nw<8, kPaged>(a, mode, grid, st);
-  else launch_nw<4, kPaged>(a, mode, grid, st);
+  else if (nw == 4) launch_nw<4, kPaged>(a, mode, grid, st);
+  else launch_nw<2, kPaged>(a, mode, grid, st);
 }
 
 static void launch_split_mode(const DecodeArgs& a, int mode, hipStream_t st) {

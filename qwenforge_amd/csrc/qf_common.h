@@ -21,6 +21,7 @@ typedef _Float16 f16;
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -70,16 +71,36 @@ __device__ __forceinline__ void rope_pair(f16x8& lo, f16x8& hi, f16x8 cos_lo, f1
 }
 
 // Reductions over the four lanes that share a query column (l ^ 16, l ^ 32).
+// gfx950's v_permlane16_swap / v_permlane32_swap exchange rows between two
+// VGPRs in the VALU: with both operands = x, the two results hold, in every
+// lane l, x[l] and x[l ^ 16] (resp. x[l ^ 32]).  No LDS round trip (a
+// ds_bpermute costs ~100+ cycles of latency on the softmax's serial chain).
+__device__ __forceinline__ void xor16_pair(float x, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ void xor32_pair(float x, float& a, float& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  a = __uint_as_float(r[0]);
+  b = __uint_as_float(r[1]);
+}
+
+// Both orders of each pair give the same fp32 result (max and + commute), so
+// every lane of a column ends with bit-identical values.
 __device__ __forceinline__ float col_max(float x) {
-  x = fmaxf(x, __shfl_xor(x, 16));
-  x = fmaxf(x, __shfl_xor(x, 32));
-  return x;
+  float a, b;
+  xor16_pair(x, a, b);
+  xor32_pair(fmaxf(a, b), a, b);
+  return fmaxf(a, b);
 }
 
 __device__ __forceinline__ float col_sum(float x) {
-  x += __shfl_xor(x, 16);
-  x += __shfl_xor(x, 32);
-  return x;
+  float a, b;
+  xor16_pair(x, a, b);
+  xor32_pair(a + b, a, b);
+  return a + b;
 }
 
 // Paged KV caches (host side): page_size must be a power of two in

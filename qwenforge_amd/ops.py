@@ -65,25 +65,33 @@ def choose_splits(batch: int, kv_heads: int, length: int, min_keys: int = 64,
 
     At least one (split, b, kv-head) workgroup per CU, the split count rounded
     up to a power of two so that splits divide into whole 32-key tiles per
-    wave, and never splits shorter than ``min_keys`` slots.  With at most 8
-    (b, kv head) pairs and splits of >= 1024 keys the count doubles, so each
-    wave keeps at most a few dependent tiles.  Measured on MI355X from 0.26 MB
-    to 268 MB of K/V (config 2: 32 splits; B=12, L=5760: 16; B=4, L=32768: 64;
-    B=16, L=32768: 8).  (The reference's rule,
+    wave, and never splits shorter than ``min_keys`` slots (twice that with 8
+    or more (b, kv head) pairs, where fewer, longer splits shorten the merge).
+    With at most 8 pairs and splits of >= 1024 keys the count doubles, so each
+    wave keeps at most a few dependent tiles.  Where 32 splits still leave
+    short splits (<= 256 keys), the count stops at 32 so that the
+    single-launch merge applies (its merging workgroup folds all S partials in
+    one pass up to S = 32).  Measured on MI355X from 0.26 MB to 268 MB of K/V
+    (config 2: 16 splits, fused; B=1, L=4096: 32, fused; B=1, L=32768: 128,
+    two launches; B=16, L=32768: 8, fused).  (The reference's rule,
     ``max(1, min(32, 272 // (B*KVH), cap // 256))`` at SE:1027, targets 68 SMs.)
     """
     pairs = max(1, batch * kv_heads)
-    by_len = max(1, math.ceil(length / min_keys))
+    by_len = max(1, math.ceil(length / (2 * min_keys if pairs >= 8 else min_keys)))
     s = 1 << max(0, math.ceil(math.log2(max(1.0, target_workgroups / pairs))))
     if pairs <= 8 and length / s >= 1024:
         s *= 2
+    if s > 32 and length <= 32 * 256:
+        s = 32
     return max(1, min(by_len, s, 1024))
 
 
 def prefer_fused(splits: int) -> bool:
-    """Single-launch merge pays off for few splits; above that the second
-    (combine) launch is cheaper than cross-XCD write-through traffic."""
-    return 1 < splits <= 8
+    """Single-launch merge (the last workgroup of each (b, kv head) merges)
+    pays off up to 32 splits, where the merging wave folds at most eight
+    partials per lane in one round trip; above that the second (combine)
+    launch is cheaper (measured on MI355X)."""
+    return 1 < splits <= 32
 
 
 def make_flash_scratch(batch: int, kv_heads: int, groups: int, capacity: int,
