@@ -144,18 +144,6 @@ __device__ __forceinline__ void lse_merge_lanes(float& M, float& L, f32x4& A) {
   A = a0;
 }
 
-// Cache policy of partial-scratch accesses in the single-launch merge: sc1,
-// the bits the gfx950 memory model gives relaxed agent-scope atomic loads and
-// stores (write-through / L2-bypassing), on 16-byte buffer accesses.
-constexpr int kSc1 = 16;
-
-// Buffer resource over `bytes` bytes at `base` (loads past the end return 0).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, int64_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
-                                           (int)(bytes < 0x7fffffff ? bytes : 0x7fffffff),
-                                           0x00020000);
-}
-
 // Folds partials j = j0, j0 + step, ... (< S) of (b, h) = bh, query q, dims
 // 4*d4 .. +3 into the running state (M, L, A), eight partials per batch with
 // every load of a batch issued before the first use.  The loads are buffer
@@ -168,9 +156,9 @@ __device__ __forceinline__ void fold_partials(const DecodeArgs& a, int bh, int q
   const int G = a.G, S = a.splits;
   const int64_t pbase = (int64_t)bh * S;
   constexpr int aux = kCoherent ? kSc1 : 0;
-  const __amdgpu_buffer_rsrc_t ra = rsrc(a.acc + pbase * G * kD, (int64_t)S * G * kD * 4);
-  const __amdgpu_buffer_rsrc_t rm = rsrc(a.m + pbase * G, (int64_t)S * G * 4);
-  const __amdgpu_buffer_rsrc_t rl = rsrc(a.l + pbase * G, (int64_t)S * G * 4);
+  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a.acc + pbase * G * kD, (int64_t)S * G * kD * 4);
+  const __amdgpu_buffer_rsrc_t rm = buffer_rsrc(a.m + pbase * G, (int64_t)S * G * 4);
+  const __amdgpu_buffer_rsrc_t rl = buffer_rsrc(a.l + pbase * G, (int64_t)S * G * 4);
   for (; j0 < S; j0 += 8 * step) {
     float mv[8], lv[8];
     f32x4 av[8];
@@ -467,7 +455,7 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
       } else if (kCoh) {
         // The resource must be wave-uniform (it lives in SGPRs): one per
         // split, the lane's query row and dims go in the offset.
-        const __amdgpu_buffer_rsrc_t ra = rsrc(a.acc + part * G * kD, (int64_t)G * kD * 4);
+        const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a.acc + part * G * kD, (int64_t)G * kD * 4);
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc), ra,
                                                (col * kD + d) * 4, 0, kSc1);
       } else {

@@ -68,6 +68,10 @@ struct Args {
   // no split (one workgroup per query tile).
   float* part;
   int split_tiles, max_parts;
+  // Single-launch merge of split query tiles: one int32 counter per
+  // [bq][query tile], zeroed by the pre-pass of the same call.  nullptr: a
+  // separate merge kernel merges the partials.
+  int* ticket;
   // Packed variable-length rows (ragged prefill): row b's tokens are
   // [cu[b], cu[b+1]) of q/k/v/out/cos/sin, whose batch strides are then 0;
   // S holds the longest row.  kv_packed: k/v are those packed inputs (1) or
@@ -602,15 +606,21 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_lds_kernel(Args a) {
   __shared__ __attribute__((aligned(16))) unsigned char k1[kBN * kRowBytes], v1[kBN * kRowBytes];
   __shared__ __attribute__((aligned(16))) unsigned char k2[kBN * kRowBytes], v2[kBN * kRowBytes];
 
-  // Work item -> (query tile, part), heaviest query tiles first, the parts of
-  // one query tile consecutive.
+  // One-dimensional grid, (work item, b * QH + q head) with the head
+  // fastest, so that the dispatcher hands out the heaviest items of every
+  // head first (a 2-D grid walks all items of head 0 before any of head 1,
+  // and the last head's heaviest items would start last).  Work item ->
+  // (query tile, part), heaviest query tiles first, the parts of one query
+  // tile consecutive.
+  const int n_bq = a.B * a.QH;
+  const int item = (int)(blockIdx.x / n_bq);
   const int n_mtiles = (a.S + kBM - 1) / kBM;
-  int mt = n_mtiles - 1 - (int)blockIdx.x, part = 0, n_parts = 1;
+  int mt = n_mtiles - 1 - item, part = 0, n_parts = 1;
   if (a.split_tiles > 0) {
     // Query tiles [g*T, g*T + T) have g + 1 parts each; walk the groups from
     // the top (the top group may be partial).
     const int T = a.split_tiles;
-    int rem = blockIdx.x, hi = n_mtiles - 1;
+    int rem = item, hi = n_mtiles - 1;
     for (;;) {
       const int g = hi / T, np = g + 1, cnt = hi - g * T + 1;
       if (rem < cnt * np || g == 0) {
@@ -623,7 +633,7 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_lds_kernel(Args a) {
       hi = g * T - 1;
     }
   }
-  const int bq = blockIdx.y;
+  const int bq = (int)(blockIdx.x % n_bq);
   const int b = bq / a.QH, hq = bq % a.QH;
   const int hk = hq / a.G;
   const int tid = threadIdx.x;
@@ -726,20 +736,77 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_lds_kernel(Args a) {
     if (kt + 2 < c.n_ktiles) lds_step<kPaged>(c, kt + 2, k2, v2, k1, v1);
   }
 
-  const float l_run = c.l4[0];
+  float l_run = c.l4[0];
   if (n_parts > 1) {
     // Partial of a split query tile: unnormalised o, running max (log2
-    // units) and sum, for the merge kernel.  Layout [bq][mt][part][row]
-    // [kPartVals]; grp 0 also writes m and l.
-    float* pp = a.part + ((((int64_t)bq * n_mtiles + mt) * a.max_parts + part) * kBM + w * 16 + col) *
-                             kPartVals;
+    // units) and sum.  Layout [bq][mt][part][row][kPartVals]; grp 0 also
+    // writes m and l.
+    const int row = w * 16 + col;
+    float* tile_parts = a.part + ((int64_t)bq * n_mtiles + mt) * a.max_parts * kBM * kPartVals;
+    if (a.ticket == nullptr) {  // merged by prefill_merge_kernel
+      float* pp = tile_parts + ((int64_t)part * kBM + row) * kPartVals;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) *reinterpret_cast<f32x4*>(pp + 16 * t + 4 * grp) = c.o[t];
-    if (grp == 0) {
-      pp[64] = c.m_use;
-      pp[65] = l_run;
+      for (int t = 0; t < 4; ++t) *reinterpret_cast<f32x4*>(pp + 16 * t + 4 * grp) = c.o[t];
+      if (grp == 0) {
+        pp[64] = c.m_use;
+        pp[65] = l_run;
+      }
+      return;
     }
-    return;
+    // Single launch: write-through (sc1) stores, wait for them, take the
+    // query tile's ticket; the part that completes the count merges every
+    // part (the others' partials through sc1 loads, its own from registers)
+    // and re-arms the ticket.
+    __shared__ int sh_last;
+    const __amdgpu_buffer_rsrc_t rp =
+        buffer_rsrc(tile_parts, (int64_t)a.max_parts * kBM * kPartVals * 4);
+    const int own = (part * kBM + row) * kPartVals;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, c.o[t]), rp,
+                                             (own + 16 * t + 4 * grp) * 4, 0, kSc1);
+    if (grp == 0) {
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, c.m_use), rp,
+                                            (own + 64) * 4, 0, kSc1);
+      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, l_run), rp,
+                                            (own + 65) * 4, 0, kSc1);
+    }
+    int* tk = a.ticket + (int64_t)bq * n_mtiles + mt;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __syncthreads();
+    if (tid == 0) sh_last = atomicAdd(tk, 1) == n_parts - 1;
+    __syncthreads();
+    if (!sh_last) return;
+    // Fold the other parts into (m_use, l_run, o), four parts per batch with
+    // all their loads issued first.
+    for (int p0 = 0; p0 < n_parts; p0 += 4) {
+      f32x4 po[4][4];
+      float pm[4], pl[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int p = p0 + u;
+        const int off = (p * kBM + row) * kPartVals;  // past the tile's slots: reads 0
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          po[u][t] = __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, (off + 16 * t + 4 * grp) * 4, 0, kSc1));
+        pm[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, (off + 64) * 4, 0, kSc1));
+        pl[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, (off + 65) * 4, 0, kSc1));
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int p = p0 + u;
+        if (p >= n_parts || p == part) continue;
+        const float mn = fmaxf(c.m_use, pm[u]);
+        const float s_old = (c.m_use == kNegInf) ? 0.f : fast_exp2(c.m_use - mn);
+        const float s_new = (pm[u] == kNegInf) ? 0.f : fast_exp2(pm[u] - mn);
+        l_run = l_run * s_old + pl[u] * s_new;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) c.o[t] = c.o[t] * s_old + po[u][t] * s_new;
+        c.m_use = mn;
+      }
+    }
+    if (tid == 0) __hip_atomic_store(tk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   if (c.qrow < S) {
     const float inv = 1.f / l_run;
@@ -829,6 +896,12 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(Args a) {
 // at slots start_pos + i (bit-exact eager rounding), so the attention kernel
 // streams finished rows.  Block = 16 tokens x (4 K chunk pairs + 8 V chunks).
 __global__ __launch_bounds__(256) void rope_kv_prefill_kernel(Args a) {
+  if (a.ticket != nullptr) {
+    // Arm the attention kernel's merge tickets (one per [bq][query tile]).
+    const int n = a.B * a.QH * ((a.S + kBM - 1) / kBM);
+    const int gid = (blockIdx.y * gridDim.x + blockIdx.x) * 256 + threadIdx.x;
+    for (int i = gid; i < n; i += gridDim.x * gridDim.y * 256) a.ticket[i] = 0;
+  }
   const int tok = blockIdx.x * 16 + (threadIdx.x >> 4);
   const int sub = threadIdx.x & 15;
   const int bh = blockIdx.y;
@@ -896,7 +969,10 @@ extern "C" int64_t qf_prefill_workspace_bytes(int B, int QH, int S) {
   split_plan(S, split_tiles, max_parts, n_items, n_merge);
   if (n_merge == 0) return 0;
   const int n_mtiles = (S + kBM - 1) / kBM;
-  return (int64_t)B * QH * n_mtiles * max_parts * kBM * kPartVals * (int64_t)sizeof(float);
+  // fp32 partials [B*QH][query tile][part][row][kPartVals], then one int32
+  // merge ticket per [B*QH][query tile].
+  return (int64_t)B * QH * n_mtiles * max_parts * kBM * kPartVals * (int64_t)sizeof(float) +
+         (int64_t)B * QH * n_mtiles * (int64_t)sizeof(int);
 }
 
 extern "C" int qf_prefill_attn(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sn,
@@ -955,7 +1031,8 @@ static int prefill_launch(Args a, bool rope, bool append, hipStream_t st) {
     int st_, mp_;
     split_plan(S, st_, mp_, n_items, n_merge);
   }
-  const dim3 lgrid(n_items, B * QH);
+  if ((int64_t)n_items * B * QH > 0x7fffffff) return QF_ERR_UNSUPPORTED;
+  const dim3 lgrid((unsigned)(n_items * B * QH));
   if (paged) {
     if (rope) hipLaunchKernelGGL((prefill_lds_kernel<true, true>), lgrid, block, 0, st, a);
     else hipLaunchKernelGGL((prefill_lds_kernel<false, true>), lgrid, block, 0, st, a);
@@ -963,7 +1040,7 @@ static int prefill_launch(Args a, bool rope, bool append, hipStream_t st) {
     if (rope) hipLaunchKernelGGL((prefill_lds_kernel<true, false>), lgrid, block, 0, st, a);
     else hipLaunchKernelGGL((prefill_lds_kernel<false, false>), lgrid, block, 0, st, a);
   }
-  if (n_merge > 0)
+  if (n_merge > 0 && a.ticket == nullptr)
     hipLaunchKernelGGL(prefill_merge_kernel, dim3(n_merge, B * QH), dim3(256), 0, st, a);
   return (int)hipGetLastError();
 }
@@ -1005,6 +1082,7 @@ static int fill_common(Args& a, const void* q, const void* k, const void* v, con
   a.part = nullptr;
   a.split_tiles = 0;
   a.max_parts = 1;
+  a.ticket = nullptr;
   a.cu = nullptr;
   a.total = 0;
   a.kv_packed = 1;
@@ -1047,6 +1125,11 @@ extern "C" int qf_prefill_attn_ws(const void* q, int64_t q_sb, int64_t q_sh, int
     a.part = static_cast<float*>(workspace);
     int n_items, n_merge;
     split_plan(S, a.split_tiles, a.max_parts, n_items, n_merge);
+    // With a pre-pass (cache append) to arm them, the tickets let the last
+    // part of each split query tile merge in the attention kernel itself.
+    if (append && n_merge > 0)
+      a.ticket = reinterpret_cast<int*>(a.part + (int64_t)B * QH * ((S + kBM - 1) / kBM) *
+                                                     a.max_parts * kBM * kPartVals);
   }
   return prefill_launch(a, rope, append, static_cast<hipStream_t>(stream));
 }

@@ -41,6 +41,20 @@ __device__ __forceinline__ void store16(f16* p, f16x8 v) {
   *reinterpret_cast<f16x8*>(p) = v;
 }
 
+// Cache policy bits of a buffer access that match a relaxed agent-scope
+// atomic load / store on gfx950 (sc1: write-through, L2-bypassing), for data
+// exchanged between workgroups of one launch (possibly on different XCDs).
+constexpr int kSc1 = 16;
+
+// Buffer resource over `bytes` bytes at `base`: accesses past the end read 0
+// and write nothing.  The resource lives in SGPRs, so `base` must be
+// wave-uniform; lane-dependent parts go in the access offset.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
+                                           (int)(bytes < 0x7fffffff ? bytes : 0x7fffffff),
+                                           0x00020000);
+}
+
 // fp16(x) for an fp32 value, round-to-nearest-even.
 __device__ __forceinline__ float round16(float x) { return (float)(f16)x; }
 

@@ -36,6 +36,46 @@ def test_config4_rope_append_s2048(dev):
     assert torch.equal(vc.cpu(), case.value)
 
 
+@pytest.mark.parametrize("seq,batch", [(1100, 2), (4100, 1)])
+def test_rope_append_single_launch_merge(dev, seq, batch):
+    """Fused RoPE + append with split query tiles (2 and 5 parts): the last
+    part of each split tile merges in the attention kernel through a ticket
+    that the pre-pass arms; three calls in a row (re-armed tickets) and a
+    graph replay must all match the oracle."""
+    case = workloads.prefill_case(seq, batch=batch, seed=seq + batch)
+    print(f"[prefill single-launch merge S={seq} B={batch}]", flush=True)
+    c = case.to(dev)
+    kc = torch.zeros(batch, 2, seq + 60, 64, dtype=torch.float16, device=dev)
+    vc = torch.zeros_like(kc)
+    q_rot = oracle.apply_rope_fp16(case.query, case.cos, case.sin)
+    k_rot = oracle.apply_rope_fp16(case.key, case.cos, case.sin)
+    ref = oracle.causal_prefill(q_rot, k_rot, case.value)
+    outs = [ops.gqa_flash_prefill_rope_append(c.query, c.key, c.value, c.cos, c.sin, kc, vc, 0)
+            for _ in range(3)]
+    torch.cuda.synchronize()
+    for out in outs:
+        assert _err(out.cpu(), ref) <= TOL
+    assert torch.equal(kc[:, :, :seq].cpu(), k_rot)
+    assert torch.equal(vc[:, :, :seq].cpu(), case.value)
+    # Graph capture (tickets and workspace at fixed addresses), several replays.
+    static_out = torch.empty_like(c.query)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        static_out.copy_(ops.gqa_flash_prefill_rope_append(c.query, c.key, c.value, c.cos, c.sin,
+                                                           kc, vc, 0))
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        static_out.copy_(ops.gqa_flash_prefill_rope_append(c.query, c.key, c.value, c.cos, c.sin,
+                                                           kc, vc, 0))
+    for _ in range(3):
+        static_out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert _err(static_out.cpu(), ref) <= TOL
+
+
 @pytest.mark.parametrize("seq", [1, 17, 64, 100, 513])
 @pytest.mark.parametrize("batch", [1, 2])
 def test_plain_prefill_ragged_lengths(dev, seq, batch):
