@@ -408,13 +408,35 @@ __device__ __forceinline__ void s_waitcnt_vm(int n) {
 }
 
 typedef __attribute__((address_space(3))) void lds_void;
-typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
-// ds_read_b64_tr_b16 of the 8-byte word at `p` (an LDS address).
-__device__ __forceinline__ f16x4 ds_read_tr16(const unsigned char* p) {
-  const i16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) i16x4*)(const_cast<unsigned char*>(p)));
-  return __builtin_bit_cast(f16x4, r);
+// 32-bit LDS address of a pointer into a __shared__ array.
+__device__ __forceinline__ unsigned lds_addr(const unsigned char* p) {
+  return (unsigned)(uintptr_t)(const lds_void*)p;
+}
+
+// LDS operand reads of a tile, written as inline asm.  The tiles arrive by
+// LDS DMA (buffer_load ... lds), which the compiler tracks with the vector
+// memory counter; it cannot tell that a read of one stage does not alias the
+// DMA into another, and before every compiler-visible LDS read it waited for
+// the DMA just issued for tile kt + 2 (vmcnt(0)), which serialised the
+// prefetch.  These reads carry no such wait: the barrier of the step orders
+// them after their own tile's DMA, and the caller waits for the reads
+// themselves with lds_wait (lgkmcnt) before the first use.
+template <int kOff>
+__device__ __forceinline__ u32x4 lds_read_b128(unsigned addr) {
+  u32x4 r;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(kOff));
+  return r;
+}
+
+// ds_read_b64_tr_b16: lane i receives the 16-bit elements that the
+// transposed 8-byte reads of its lane group place there (the V^T operand).
+template <int kOff>
+__device__ __forceinline__ u32x2 lds_read_tr_b64(unsigned addr) {
+  u32x2 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "i"(kOff));
+  return r;
 }
 
 // Per-lane state of the streaming prefill, shared by the three unrolled steps.
@@ -438,8 +460,12 @@ struct LdsCtx {
   int64_t k_sp, v_sp, start;   // page strides (bytes), first slot of the sequence
   int pid, pwin, kt_issue, log2p, ppr, n_pages;
   int S, mt, qrow, n_ktiles, grp, lrow0, pch, w;
-  int koff[2][2][2];  // [ch][j][kk] LDS byte offsets of the K operand reads
-  int voff[2][4][2];  // [ch][d tile][h] LDS byte offsets of the V^T reads
+  // LDS byte offsets of the operand reads for ch = 0, j = 0 (K) and
+  // ch = 0, h = 0 (V^T); the other (ch, j / h) add the row offsets
+  // (32 ch + 4 j) * 128 (resp. 4 h), which leave the swizzle unchanged, as
+  // immediates.
+  int koff[2];  // [kk]
+  int voff[4];  // [d tile]
   f16x8 qf[2];
   float m_use, ks2;
   f32x4 l4;   // running sum of p per query column, kept by an MFMA against ones
@@ -534,14 +560,37 @@ __device__ __forceinline__ void lds_step(LdsCtx& c, int kt, const unsigned char*
   __builtin_amdgcn_s_barrier();
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 
+  // K operands of tile kt, then (in flight under the score MFMAs and the
+  // softmax) its V^T operands.
+  const unsigned ks = lds_addr(Ks), vs = lds_addr(Vs);
+  u32x4 kr[2][2][2];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    const unsigned ka0 = ks + c.koff[kk];
+    kr[0][0][kk] = lds_read_b128<0>(ka0);
+    kr[0][1][kk] = lds_read_b128<4 * kRowBytes>(ka0);
+    kr[1][0][kk] = lds_read_b128<32 * kRowBytes>(ka0);
+    kr[1][1][kk] = lds_read_b128<36 * kRowBytes>(ka0);
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(kr[0][0][0]), "+v"(kr[0][0][1]), "+v"(kr[0][1][0]), "+v"(kr[0][1][1]),
+                 "+v"(kr[1][0][0]), "+v"(kr[1][0][1]), "+v"(kr[1][1][0]), "+v"(kr[1][1][1]));
+  u32x2 vr[2][4][2];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const unsigned va0 = vs + c.voff[t];
+    vr[0][t][0] = lds_read_tr_b64<0>(va0);
+    vr[0][t][1] = lds_read_tr_b64<4 * kRowBytes>(va0);
+    vr[1][t][0] = lds_read_tr_b64<32 * kRowBytes>(va0);
+    vr[1][t][1] = lds_read_tr_b64<36 * kRowBytes>(va0);
+  }
   f16x8 ka[2][2][2];
 #pragma unroll
   for (int ch = 0; ch < 2; ++ch)
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-        ka[ch][j][kk] = *reinterpret_cast<const f16x8*>(Ks + c.koff[ch][j][kk]);
+      for (int kk = 0; kk < 2; ++kk) ka[ch][j][kk] = __builtin_bit_cast(f16x8, kr[ch][j][kk]);
   // Refill after the K operands are in registers (the V^T reads come later).
   if (kt + 2 < c.n_ktiles) lds_issue<kPaged>(c, Kn, Vn);  // tile kt + 2
   f32x4 sc[4];
@@ -587,12 +636,17 @@ __device__ __forceinline__ void lds_step(LdsCtx& c, int kt, const unsigned char*
   const f16x8 ones = {(f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f, (f16)1.f};
   c.l4 = mfma16x16x32(ones, pb[0], c.l4);
   c.l4 = mfma16x16x32(ones, pb[1], c.l4);
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(vr[0][0][0]), "+v"(vr[0][0][1]), "+v"(vr[0][1][0]), "+v"(vr[0][1][1]),
+                 "+v"(vr[0][2][0]), "+v"(vr[0][2][1]), "+v"(vr[0][3][0]), "+v"(vr[0][3][1]),
+                 "+v"(vr[1][0][0]), "+v"(vr[1][0][1]), "+v"(vr[1][1][0]), "+v"(vr[1][1][1]),
+                 "+v"(vr[1][2][0]), "+v"(vr[1][2][1]), "+v"(vr[1][3][0]), "+v"(vr[1][3][1]));
 #pragma unroll
   for (int ch = 0; ch < 2; ++ch)
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const f16x4 lo = ds_read_tr16(Vs + c.voff[ch][t][0]);
-      const f16x4 hi = ds_read_tr16(Vs + c.voff[ch][t][1]);
+      const f16x4 lo = __builtin_bit_cast(f16x4, vr[ch][t][0]);
+      const f16x4 hi = __builtin_bit_cast(f16x4, vr[ch][t][1]);
       const f16x8 va = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       c.o[t] = mfma16x16x32(va, pb[ch], c.o[t]);
     }
@@ -706,24 +760,20 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_lds_kernel(Args a) {
   if (kt0 + 1 < c.n_ktiles) lds_issue<kPaged>(c, k1, v1);  // tile kt0 + 1
   if (kRopeQ) rope_pair(c.qf[0], c.qf[1], qcs[0], qcs[1], qcs[2], qcs[3]);
 
+  {
+    // K operand row r = 32 ch + 8 (col / 4) + 4 j + col % 4 and V^T row
+    // r = 32 ch + 8 grp + 4 h + col / 4: ch and j / h set bits 5 and 2 of r,
+    // which the swizzle (bits 1, 3, 4) does not read.
+    const int rk = 8 * (col >> 2) + (col & 3);
 #pragma unroll
-  for (int ch = 0; ch < 2; ++ch)
+    for (int kk = 0; kk < 2; ++kk) c.koff[kk] = rk * kRowBytes + 16 * ((grp + 4 * kk) ^ swz(rk));
+    const int rv = 8 * grp + (col >> 2);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int r = 32 * ch + 8 * (col >> 2) + 4 * j + (col & 3);
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) c.koff[ch][j][kk] = r * kRowBytes + 16 * ((grp + 4 * kk) ^ swz(r));
+    for (int t = 0; t < 4; ++t) {
+      const int d = 16 * t + 4 * (col & 3);
+      c.voff[t] = rv * kRowBytes + 16 * ((d >> 3) ^ swz(rv)) + 2 * (d & 7);
     }
-#pragma unroll
-  for (int ch = 0; ch < 2; ++ch)
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int r = 32 * ch + 8 * grp + 4 * h + (col >> 2);
-        const int d = 16 * t + 4 * (col & 3);
-        c.voff[ch][t][h] = r * kRowBytes + 16 * ((d >> 3) ^ swz(r)) + 2 * (d & 7);
-      }
+  }
   c.m_use = kNegInf;
   c.l4 = f32x4{0.f, 0.f, 0.f, 0.f};
   c.ks2 = a.scale_log2;
