@@ -145,11 +145,16 @@ int qf_prefill_attn(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sn,
 
 /*
  * qf_prefill_attn with a caller-owned workspace that lets the heaviest query
- * tiles split their key range over two workgroups (the causal prefill's
- * longest chain is the last query tile's; split, it halves).  The split
- * query tiles write fp32 partials to `workspace` and a second launch merges
- * them into `out`; the result is the same attention up to fp32 summation
- * order.  workspace == NULL (or workspace_bytes == 0) is qf_prefill_attn.
+ * tiles split their key range over several workgroups of at most 16 key
+ * tiles (the causal prefill's longest chain is the last query tile's; split,
+ * it is bounded).  The split query tiles write fp32 partials to `workspace`;
+ * with the cache append (k_cache/v_cache given) the last part of each split
+ * tile merges them in the attention launch through per-tile counters at the
+ * end of the workspace, which the call arms itself (the workspace needs no
+ * initialisation); otherwise a second launch merges them.  The result is the
+ * same attention up to fp32 summation order.  Calls that share a workspace
+ * must not overlap.  workspace == NULL (or workspace_bytes == 0) is
+ * qf_prefill_attn.
  * A non-NULL workspace must be 16-byte aligned and at least
  * qf_prefill_workspace_bytes(B, QH, S) bytes, else QF_ERR_INVALID_ARG.
  * No counterpart in the reference (its Triton kernel has one program per

@@ -112,21 +112,22 @@ class PagedDecodeEngine(DecodeEngine):
         rope = (pos, self.inv_freq)                              # each row's own position
         hidden, q_rot, h = ctx["hidden"], ctx["q_rot"], ctx["h"]
         for i, (layer, (kp, vp)) in enumerate(zip(self.w["layers"], kv.pools)):
+            w_qkv, w_gate_up = self.projection_weights(i, b)
             if i == 0:
                 paged.rms_qkv_rope_append_paged(self.w["embed"], layer["input_norm"], eps,
-                                                layer["qkv_weight"], layer["qkv_bias"], None, None,
+                                                w_qkv, layer["qkv_bias"], None, None,
                                                 kp, vp, table, pos, q_rot, token=ctx["token"],
                                                 hidden_out=hidden, positions=rope)
             else:
                 paged.rms_qkv_rope_append_paged(hidden, layer["input_norm"], eps,
-                                                layer["qkv_weight"], layer["qkv_bias"], None, None,
+                                                w_qkv, layer["qkv_bias"], None, None,
                                                 kp, vp, table, pos, q_rot, positions=rope)
             grouped = q_rot.view(b, cfg.kv_heads, cfg.groups, cfg.head_dim)
             # The slot just written is the row's last valid one.
             paged.flash_decode_split_paged(grouped, kp, vp, table, None, ctx["flash"], kv_last=pos,
                                            scale=self.scale)
             step_ops.attn_merge_o_proj(ctx["flash"], layer["o_weight"], hidden)
-            step_ops.rms_gate_up_swiglu(hidden, layer["post_norm"], eps, layer["gate_up_weight"], h)
+            step_ops.rms_gate_up_swiglu(hidden, layer["post_norm"], eps, w_gate_up, h)
             step_ops.gemv_residual(h, layer["down_weight"], hidden)
         step_ops.rms_lm_head(hidden, self.w["final_norm"], eps, self.w["lm_head"], ctx["logits"],
                              ctx["keys"])

@@ -142,9 +142,11 @@ def test_prefill_workspace_plan():
     lib = _lib.load()
     # Short prompts (<= 16 query tiles) are not split; at S=2048 (32 query
     # tiles of up to 32 key tiles) a query tile has at most 2 parts of <= 16.
+    # After the fp32 partials comes one int32 merge ticket per query tile.
     assert lib.qf_prefill_workspace_bytes(1, 14, 1024) == 0
-    assert lib.qf_prefill_workspace_bytes(1, 14, 2048) == 14 * 32 * 2 * 64 * 66 * 4
-    assert lib.qf_prefill_workspace_bytes(2, 14, 4096) == 2 * 14 * 64 * 4 * 64 * 66 * 4
+    assert lib.qf_prefill_workspace_bytes(1, 14, 2048) == 14 * 32 * 2 * 64 * 66 * 4 + 14 * 32 * 4
+    assert (lib.qf_prefill_workspace_bytes(2, 14, 4096) ==
+            2 * 14 * 64 * 4 * 64 * 66 * 4 + 2 * 14 * 64 * 4)
     # A workspace smaller than the plan is rejected before any launch.
     rc = lib.qf_prefill_attn_ws(16, 0, 0, 0, 16, 0, 0, 0, 16, 0, 0, 0, None, None, 0, 0,
                                 None, 0, 0, 0, None, 0, 0, 0, 0, 0, 16, 0, 0, 0,

@@ -142,6 +142,45 @@ def test_fused_step_matches_torch_step(dev):
         assert (vf - vt).abs().max().item() <= 2e-2
 
 
+@pytest.mark.parametrize("b", [2, 4])
+def test_tile_weights_step_matches_row_weights(dev, b):
+    """From 2 rows the fused step reads QKV and gate/up as matrix-core tiles;
+    teacher-forced logits, appended cache rows and bookkeeping match the
+    row-major (dot-product) kernels."""
+    cfg = Qwen2Config(layers=3)
+    w = init_weights(cfg, dev, seed=9)
+    s, steps = 130, 3
+    gen = torch.Generator().manual_seed(11)
+    ids = torch.randint(0, cfg.vocab, (b, s), generator=gen).to(dev)
+    teacher = torch.randint(0, cfg.vocab, (steps, b), generator=gen).to(dev)
+    out = {}
+    for tiles in (True, False):
+        eng = DecodeEngine(cfg, w, dev, tile_weights=tiles)
+        caches = eng.new_caches(b, 192)
+        eng.prefill(ids, caches)
+        ctx = eng.make_context(caches, b, steps + 1)
+        assert ctx["fused"]
+        ctx["pos"].fill_(s)
+        ctx["write"].fill_(s)
+        ctx["step"].fill_(1)
+        logits = []
+        for t in range(steps):
+            ctx["token"].copy_(teacher[t])
+            eng._step(ctx)
+            logits.append(ctx["logits"].float().cpu())
+        torch.cuda.synchronize()
+        assert (eng._tiles is not None) == tiles
+        out[tiles] = (torch.stack(logits), int(ctx["write"].item()), ctx["pos"].cpu(),
+                      [k[:, :, s:s + steps].float().cpu() for k, _ in caches])
+    (lt, wt, pt, ct), (lr, wr, pr, cr) = out[True], out[False]
+    err = (lt - lr).abs().max().item()
+    print(f"[tile vs row weights B={b}] max|dlogit| {err:.3e}", flush=True)
+    assert err <= LOGIT_TOL
+    assert wt == wr == s + steps and torch.equal(pt, pr)
+    for kt, kr in zip(ct, cr):
+        assert (kt - kr).abs().max().item() <= 2e-2
+
+
 def test_ragged_prefill_and_decode_match_oracle(dev):
     """Variable-length prompts: packed prefill == per-row oracle prefill
     (SE:1186-1202), then teacher-forced decode over the bias-masked holes
