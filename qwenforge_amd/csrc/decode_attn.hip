@@ -418,6 +418,11 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
   // 16-dim slices t = w', w' + NW, ... and stores them from the MFMA layout
   // (lane (q, grp) holds dims 16t + 4grp .. +3 of query q).  Two barriers;
   // each LDS pass is one round of independent accesses.
+  // Only the first nact waves saw a tile (the split is shorter than NW
+  // tiles, e.g. when the single-launch merge asks for a wave per query):
+  // the others hold an empty state and take no part in the exchange.
+  int nact = (hi - lo + kTile - 1) / kTile;
+  nact = nact < 1 ? 1 : (nact > NW ? NW : nact);
   if (grp == 0) {
     sm_ml[0][w][col] = m_run;
     sm_ml[1][w][col] = l_run;
@@ -425,18 +430,22 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
   __syncthreads();  // (m, l) visible; every wave is done with its V tiles
   float M = kNegInf;
 #pragma unroll
-  for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, sm_ml[0][ww][col]);
+  for (int ww = 0; ww < NW; ++ww)
+    if (ww < nact) M = fmaxf(M, sm_ml[0][ww][col]);
   const float safe = (M == kNegInf) ? 0.f : M;
   float L = 0.f;
 #pragma unroll
   for (int ww = 0; ww < NW; ++ww) {
+    if (ww >= nact) break;
     const float mw = sm_ml[0][ww][col];
     L += ((mw == kNegInf) ? 0.f : fast_exp2(mw - safe)) * sm_ml[1][ww][col];
   }
   const float wt = (m_run == kNegInf) ? 0.f : fast_exp2(m_run - safe);
   f32x4* sm_o = reinterpret_cast<f32x4*>(lds_raw);  // [NW][4][64]
+  if (w < nact) {
 #pragma unroll
-  for (int t = 0; t < 4; ++t) sm_o[(w * 4 + t) * 64 + lane] = o[t] * wt;
+    for (int t = 0; t < 4; ++t) sm_o[(w * 4 + t) * 64 + lane] = o[t] * wt;
+  }
   __syncthreads();
 
   const int S = a.splits, G = a.G;
@@ -444,7 +453,8 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
   for (int t = w; t < 4; t += NW) {
     f32x4 acc = sm_o[t * 64 + lane];
 #pragma unroll
-    for (int ww = 1; ww < NW; ++ww) acc += sm_o[(ww * 4 + t) * 64 + lane];
+    for (int ww = 1; ww < NW; ++ww)
+      if (ww < nact) acc += sm_o[(ww * 4 + t) * 64 + lane];
     if (col < G) {
       const int d = 16 * t + 4 * grp;
       if (kMode == kDirect) {
