@@ -416,17 +416,30 @@ def _traffic():
         return json.load(f).get("traffic_bytes_per_launch")
 
 
-def cpu_baseline(layers, seconds):
-    """The CPU oracle (fp32 restatement of SE:939-972) on config-2 layers, host cores."""
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _time_oracle(layers, seconds, threads):
+    """Config-2 layer calls of the CPU oracle for about `seconds` at `threads`
+    threads (3 warm-up calls first); returns (GB/s, calls, median s, total s)."""
     import torch
 
     import oracle
 
-    threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
+    for c in layers[:3]:
+        oracle.grouped_decode_attention(c.grouped, c.key_cache, c.value_cache, c.bias)
     t_end = time.perf_counter() + seconds
     done_bytes, n_layers, times = 0, 0, []
-    while time.perf_counter() < t_end or n_layers < 3:
+    while time.perf_counter() < t_end or n_layers < 20:
         c = layers[n_layers % len(layers)]
         t0 = time.perf_counter()
         oracle.grouped_decode_attention(c.grouped, c.key_cache, c.value_cache, c.bias)
@@ -434,13 +447,26 @@ def cpu_baseline(layers, seconds):
         done_bytes += c.valid_bytes
         n_layers += 1
     total = sum(times)
+    return done_bytes / total / 1e9, n_layers, statistics.median(times), total
+
+
+def cpu_baseline(layers, seconds):
+    """The CPU oracle (fp32 restatement of SE:939-972) on config-2 layers,
+    timed on the host's cores (all affine threads; then one thread on a
+    third of the time budget)."""
+    threads = len(os.sched_getaffinity(0))
+    gbs, n, med, total = _time_oracle(layers, seconds, threads)
+    gbs1, n1, med1, total1 = _time_oracle(layers, seconds / 3, 1)
     return {
-        "value": round(done_bytes / total / 1e9, 3),
+        "value": round(gbs, 3),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{n_layers} config-2 layer calls (B=4 ragged, fp32 oracle), "
-                  f"median {statistics.median(times) * 1e6:.0f} us/layer, {total:.1f} s total",
+        "sample": f"{n} config-2 layer calls (B=4 ragged, fp32 oracle), "
+                  f"median {med * 1e6:.0f} us/layer, {total:.1f} s total",
+        "single_thread": {"value": round(gbs1, 3), "unit": "GB/s",
+                          "sample": f"{n1} calls, median {med1 * 1e6:.0f} us/layer, {total1:.1f} s"},
+        "cpu_model": _cpu_model(),
     }
 
 
