@@ -475,13 +475,21 @@ def gqa_flash_prefill_rope_append(query: torch.Tensor, key: torch.Tensor, value:
     Rotates q and k with the fp16 tables ``cos``/``sin`` ((S, D), (B, S, D) or
     (B, 1, S, D); SE:545-548), attends causally, writes the rotated k and the
     raw v to ``cache[:, :, start_pos:start_pos+S]`` (SE:715-716) and returns
-    the attention output (B, QH, S, D).
+    the attention output (B, QH, S, D), stored token-major ((B, S, QH, D)
+    memory order, the layout o_proj consumes: ``out.transpose(1, 2)`` is
+    contiguous, so the reshape to (B, S, hidden) copies nothing).
     """
-    out = torch.empty(query.shape, device=query.device, dtype=query.dtype)
-    return _prefill_launch(query, key, value, out, cos, sin, key_cache, value_cache, start_pos)
+    return _prefill_launch(query, key, value, _token_major_out(query), cos, sin, key_cache,
+                           value_cache, start_pos)
+
+
+def _token_major_out(query: torch.Tensor) -> torch.Tensor:
+    """Uninitialised (B, QH, S, D) tensor laid out as (B, S, QH, D)."""
+    b, qh, s, d = query.shape
+    return torch.empty((b, s, qh, d), device=query.device, dtype=query.dtype).transpose(1, 2)
 
 
 @gqa_flash_prefill_rope_append.register_fake
 def _gqa_flash_prefill_rope_append_fake(query, key, value, cos, sin, key_cache, value_cache,
                                         start_pos):
-    return torch.empty(query.shape, device=query.device, dtype=query.dtype)
+    return _token_major_out(query)
