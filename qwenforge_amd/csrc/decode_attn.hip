@@ -73,18 +73,13 @@ struct DecodeArgs {
   int log2p, n_pages;
 };
 
-// Partial-scratch accesses.  kCoherent: relaxed agent-scope atomics, which
-// the compiler emits as write-through / cache-bypassing (sc1) accesses, so a
-// workgroup on another XCD sees them without an L2 writeback.
+// Partial-scratch stores.  kCoherent: a relaxed agent-scope atomic store,
+// which the compiler emits as a write-through (sc1) store, so a workgroup on
+// another XCD sees it without an L2 writeback.
 template <bool kCoherent>
 __device__ __forceinline__ void st(float* p, float v) {
   if (kCoherent) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   else *p = v;
-}
-template <bool kCoherent>
-__device__ __forceinline__ float ld(const float* p) {
-  if (kCoherent) return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return *p;
 }
 
 // Slot range [lo, hi) of split `s` for batch row `b`: the row's valid slots
