@@ -63,22 +63,29 @@ def choose_splits(batch: int, kv_heads: int, length: int, min_keys: int = 64,
                   target_workgroups: int = NUM_CUS) -> int:
     """Split count for the decode kernel on MI355X.
 
-    At least one (split, b, kv-head) workgroup per CU, the split count rounded
-    up to a power of two so that splits divide into whole 32-key tiles per
-    wave, and never splits shorter than ``min_keys`` slots (twice that with 8
-    or more (b, kv head) pairs, where fewer, longer splits shorten the merge).
-    With at most 8 pairs and splits of >= 1024 keys the count doubles, so each
-    wave keeps at most a few dependent tiles.  Where 32 splits still leave
-    short splits (<= 256 keys), the count stops at 32 so that the
-    single-launch merge applies (its merging workgroup folds all S partials in
-    one pass up to S = 32).  Measured on MI355X from 0.26 MB to 268 MB of K/V
-    (config 2: 16 splits, fused; B=1, L=4096: 32, fused; B=1, L=32768: 128,
-    two launches; B=16, L=32768: 8, fused).  (The reference's rule,
+    The (split, b, kv-head) workgroups fill the CUs once -- floor(CUs / pairs)
+    splits -- or twice (two eight-wave workgroups share a CU) when that still
+    allows the single-launch merge (<= 32 splits) and keeps splits at <= 512
+    keys; a count just above one per CU leaves a few CUs with a second
+    workgroup and costs up to 30% (measured: B=12 L=5760 at 11 splits, 264
+    workgroups, 16.7 us vs 13.1 us at 10).  Splits are never shorter than
+    ``min_keys`` slots (twice that with 8 or more (b, kv head) pairs, where
+    fewer, longer splits shorten the merge).  With at most 8 pairs and splits
+    of >= 1024 keys the count doubles, so each wave keeps at most a few
+    dependent tiles.  Where 32 splits still leave short splits (<= 256 keys),
+    the count stops at 32 so that the single-launch merge applies (its merging
+    workgroup folds all S partials in one pass up to S = 32).  Measured on
+    MI355X from 0.26 MB to 268 MB of K/V (config 2: 16 splits, fused; B=1,
+    L=4096: 32, fused; B=1, L=32768: 128, two launches; B=16, L=32768: 8,
+    fused; B=12, L=5760: 21, fused).  (The reference's rule,
     ``max(1, min(32, 272 // (B*KVH), cap // 256))`` at SE:1027, targets 68 SMs.)
     """
     pairs = max(1, batch * kv_heads)
     by_len = max(1, math.ceil(length / (2 * min_keys if pairs >= 8 else min_keys)))
-    s = 1 << max(0, math.ceil(math.log2(max(1.0, target_workgroups / pairs))))
+    s = max(1, target_workgroups // pairs)
+    s2 = 2 * target_workgroups // pairs
+    if 1 < s2 <= 32 and length <= 512 * s2:
+        s = s2
     if pairs <= 8 and length / s >= 1024:
         s *= 2
     if s > 32 and length <= 32 * 256:
