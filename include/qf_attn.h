@@ -131,6 +131,9 @@ int qf_decode_combine(const float* acc, const float* m, const float* l, int spli
  *   k_cache, v_cache (B, KVH, cap, D): the post-RoPE k and the raw v of token
  *          i are written to slot start_pos + i (the slice copy of
  *          SE:715-716); both or neither.  Requires start_pos + S <= cap.
+ *
+ * Needs no scratch memory: one workgroup per 64-row query tile, the key
+ * range split over its two halves of waves and merged in LDS.
  */
 int qf_prefill_attn(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sn,
                     const void* k, int64_t k_sb, int64_t k_sh, int64_t k_sn,
@@ -143,37 +146,6 @@ int qf_prefill_attn(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sn,
                     int B, int QH, int KVH, int S, int D, float scale,
                     void* stream);
 
-/*
- * qf_prefill_attn with a caller-owned workspace that lets the heaviest query
- * tiles split their key range over several workgroups of at most 16 key
- * tiles (the causal prefill's longest chain is the last query tile's; split,
- * it is bounded).  The split query tiles write fp32 partials to `workspace`;
- * with the cache append (k_cache/v_cache given) the last part of each split
- * tile merges them in the attention launch through per-tile counters at the
- * end of the workspace, which the call arms itself (the workspace needs no
- * initialisation); otherwise a second launch merges them.  The result is the
- * same attention up to fp32 summation order.  Calls that share a workspace
- * must not overlap.  workspace == NULL (or workspace_bytes == 0) is
- * qf_prefill_attn.
- * A non-NULL workspace must be 16-byte aligned and at least
- * qf_prefill_workspace_bytes(B, QH, S) bytes, else QF_ERR_INVALID_ARG.
- * No counterpart in the reference (its Triton kernel has one program per
- * query tile, SE:276-280); the op wrapper allocates the workspace.
- */
-int qf_prefill_attn_ws(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sn,
-                       const void* k, int64_t k_sb, int64_t k_sh, int64_t k_sn,
-                       const void* v, int64_t v_sb, int64_t v_sh, int64_t v_sn,
-                       const void* cos, const void* sin, int64_t cs_sb, int64_t cs_sn,
-                       void* k_cache, int64_t kc_sb, int64_t kc_sh, int64_t kc_sn,
-                       void* v_cache, int64_t vc_sb, int64_t vc_sh, int64_t vc_sn,
-                       int64_t start_pos, int cap,
-                       void* out, int64_t o_sb, int64_t o_sh, int64_t o_sn,
-                       int B, int QH, int KVH, int S, int D, float scale,
-                       void* workspace, int64_t workspace_bytes, void* stream);
-
-/* Workspace bytes qf_prefill_attn_ws uses for (B, QH, S); 0 when the shape
- * gains nothing from splitting (short prompts). */
-int64_t qf_prefill_workspace_bytes(int B, int QH, int S);
 
 /*
  * Ragged (variable-length) causal prefill of B packed rows, with the same

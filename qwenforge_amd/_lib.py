@@ -57,20 +57,6 @@ SIGNATURES = {
         _i32, _i32, _i32, _i32, _i32,   # B, QH, KVH, S, D
         _f32, _vp,                      # scale, stream
     ],
-    "qf_prefill_attn_ws": [
-        _vp, _i64, _i64, _i64,          # q
-        _vp, _i64, _i64, _i64,          # k
-        _vp, _i64, _i64, _i64,          # v
-        _vp, _vp, _i64, _i64,           # cos, sin, cs_sb, cs_sn
-        _vp, _i64, _i64, _i64,          # k_cache
-        _vp, _i64, _i64, _i64,          # v_cache
-        _i64, _i32,                     # start_pos, cap
-        _vp, _i64, _i64, _i64,          # out
-        _i32, _i32, _i32, _i32, _i32,   # B, QH, KVH, S, D
-        _f32,                           # scale
-        _vp, _i64, _vp,                 # workspace, workspace_bytes, stream
-    ],
-    "qf_prefill_workspace_bytes": [_i32, _i32, _i32],
     "qf_prefill_varlen": [
         _vp, _i64, _i64,                # q, q_sh, q_sn
         _vp, _i64, _i64,                # k
@@ -219,7 +205,7 @@ SIGNATURES = {
 }
 
 # Entry points that do not return an int status.
-RESTYPES = {"qf_error_string": C.c_char_p, "qf_prefill_workspace_bytes": C.c_int64}
+RESTYPES = {"qf_error_string": C.c_char_p}
 
 _lock = threading.Lock()
 _lib: C.CDLL | None = None

@@ -12,4 +12,4 @@ extern "C" const char* qf_error_string(int code) {
   return "unknown error";
 }
 
-extern "C" int qf_abi_version(void) { return 102; }
+extern "C" int qf_abi_version(void) { return 200; }

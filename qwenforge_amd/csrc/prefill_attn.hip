@@ -6,13 +6,20 @@
 // RoPE in front of it (:767, :542-554) and the slice append of the cached
 // prefill (:715-716).
 //
-// One workgroup = 64 query rows of one query head (four wave64s x 16 rows);
-// query tiles are launched heaviest-first (the last rows see the most keys).
-// K/V tiles of 64 keys are double-buffered in LDS: while the waves compute on
-// tile t, the registers already hold tile t+1's global loads, which are
-// rotated (K) and written to the other LDS buffer afterwards, so one barrier
-// per tile separates the phases and HBM latency overlaps the MFMA work.
-// Per 64-key tile the workgroup
+// Two kernels, both over query tiles of 64 rows launched heaviest-first (the
+// last rows see the most keys), 16 query rows per wave:
+//   prefill_lds2_kernel (every call with a cache to append to, and every call
+//     without RoPE): a pre-pass writes rotated K and raw V to the cache, then
+//     one workgroup of eight waves per query tile streams the key tiles back
+//     from the cache into LDS with direct-to-LDS loads, the even tiles to
+//     waves 0-3 and the odd ones to waves 4-7, which merge at the end;
+//   prefill_kernel (RoPE without a cache): four waves per query tile, K
+//     rotated in registers on its way to LDS.
+// prefill_kernel: K/V tiles of 64 keys are double-buffered in LDS: while the
+// waves compute on tile t, the registers already hold tile t+1's global
+// loads, which are rotated (K) and written to the other LDS buffer
+// afterwards, so one barrier per tile separates the phases and HBM latency
+// overlaps the MFMA work.  Per 64-key tile the workgroup
 //   - loads K with 16-byte loads, applies RoPE in registers (both halves of a
 //     rotate-half pair are loaded by the same thread), stores the rotated rows
 //     to LDS in natural [key][d] layout,
@@ -61,17 +68,6 @@ struct Args {
   int64_t o_sb, o_sh, o_sn;
   int B, QH, KVH, G, S;
   float scale_log2;
-  // Split-K of long query tiles (LDS kernel only): query tile mt, with
-  // n = mt + 1 key tiles, runs as P = ceil(n / split_tiles) workgroups over
-  // equal key-tile ranges; when P > 1 each writes an fp32 partial to `part`
-  // (slot [bq][mt][p], p < max_parts) for the merge kernel.  split_tiles == 0:
-  // no split (one workgroup per query tile).
-  float* part;
-  int split_tiles, max_parts;
-  // Single-launch merge of split query tiles: one int32 counter per
-  // [bq][query tile], zeroed by the pre-pass of the same call.  nullptr: a
-  // separate merge kernel merges the partials.
-  int* ticket;
   // Packed variable-length rows (ragged prefill): row b's tokens are
   // [cu[b], cu[b+1]) of q/k/v/out/cos/sin, whose batch strides are then 0;
   // S holds the longest row.  kv_packed: k/v are those packed inputs (1) or
@@ -380,8 +376,9 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(Args a) {
 // ---------------------------------------------------------------------------
 // Streaming variant for K/V that are already rotated (and, in the fused op,
 // already in the cache): tiles go HBM -> LDS with asynchronous 16-byte
-// direct-to-LDS loads (global_load_lds) into a three-stage ring, so no
-// registers stage the data and two tiles are always in flight.  LDS rows are
+// direct-to-LDS loads (buffer_load ... lds), so no registers stage the data
+// and the next tiles are in flight while the current ones are computed.
+// LDS rows are
 // 128 bytes, XOR-swizzled in 16-byte chunks (chunk c of row r lives at
 // c ^ swz(r)).  gfx950's LDS serves 256 bytes per cycle (64 banks of 4
 // bytes: a 16-byte read takes 16 lanes at a time).  With
@@ -392,9 +389,7 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(Args a) {
 // from ds_read_b64_tr_b16: within each 16-lane group, lane i receives element
 // i % 4 of the 8-byte words addressed by lanes 4t + i/4 (t = 0..3), so lanes
 // that address 4 keys x 16 dims of V receive V^T[d][4 keys] directly.
-constexpr int kStages = 3;
 constexpr int kRowBytes = kD * 2;  // 128
-constexpr int kPartVals = kD + 2;  // per query row of a split partial: o[64], m, l
 
 __device__ __forceinline__ int swz(int row) {
   const int r1 = (row >> 1) & 1, r3 = (row >> 3) & 1, r4 = (row >> 4) & 1;
@@ -418,11 +413,11 @@ __device__ __forceinline__ unsigned lds_addr(const unsigned char* p) {
 // LDS operand reads of a tile, written as inline asm.  The tiles arrive by
 // LDS DMA (buffer_load ... lds), which the compiler tracks with the vector
 // memory counter; it cannot tell that a read of one stage does not alias the
-// DMA into another, and before every compiler-visible LDS read it waited for
-// the DMA just issued for tile kt + 2 (vmcnt(0)), which serialised the
+// DMA into another, and before every compiler-visible LDS read it would wait
+// for the DMA just issued for the next tiles (vmcnt(0)), which serialises the
 // prefetch.  These reads carry no such wait: the barrier of the step orders
 // them after their own tile's DMA, and the caller waits for the reads
-// themselves with lds_wait (lgkmcnt) before the first use.
+// themselves (lgkmcnt) before the first use.
 template <int kOff>
 __device__ __forceinline__ u32x4 lds_read_b128(unsigned addr) {
   u32x4 r;
@@ -439,7 +434,7 @@ __device__ __forceinline__ u32x2 lds_read_tr_b64(unsigned addr) {
   return r;
 }
 
-// Per-lane state of the streaming prefill, shared by the three unrolled steps.
+// Per-lane state of the streaming prefill, shared by its tile steps.
 struct LdsCtx {
   const f16* kb;
   const f16* vb;
@@ -459,7 +454,7 @@ struct LdsCtx {
   const int32_t* trow;
   int64_t k_sp, v_sp, start;   // page strides (bytes), first slot of the sequence
   int pid, pwin, kt_issue, log2p, ppr, n_pages;
-  int S, mt, qrow, n_ktiles, grp, lrow0, pch, w;
+  int S, mt, qrow, grp, lrow0, pch, w;
   // LDS byte offsets of the operand reads for ch = 0, j = 0 (K) and
   // ch = 0, h = 0 (V^T); the other (ch, j / h) add the row offsets
   // (32 ch + 4 j) * 128 (resp. 4 h), which leave the swizzle unchanged, as
@@ -493,10 +488,10 @@ __device__ __forceinline__ void load_pids(LdsCtx& c, int win) {
 }
 
 // Async loads of the next tile (this wave's 16 rows of K and of V) into
-// (Kd, Vd); advances the issue cursor by one tile (scalar adds only).  Paged
+// (Kd, Vd); advances the issue cursor by kAdv tiles (scalar adds only).  Paged
 // caches: the tile's rows lie in one page (start and the page size are
 // multiples of 64), whose base comes from the page ids held in `pid`.
-template <bool kPaged>
+template <bool kPaged, int kAdv = 1>
 __device__ __forceinline__ void lds_issue(LdsCtx& c, unsigned char* Kd, unsigned char* Vd) {
   if (kPaged) {
     const int64_t slot0 = c.start + (int64_t)c.kt_issue * kBN;
@@ -506,7 +501,7 @@ __device__ __forceinline__ void lds_issue(LdsCtx& c, unsigned char* Kd, unsigned
     const int64_t row = slot0 & ((1 << c.log2p) - 1);
     c.knext = c.kpool + (int64_t)page * c.k_sp + row * c.k_sn * 2;
     c.vnext = c.vpool + (int64_t)page * c.v_sp + row * c.v_sn * 2;
-    ++c.kt_issue;
+    c.kt_issue += kAdv;
   }
   const __amdgpu_buffer_rsrc_t rk = tile_rsrc(c.knext, c.krem);
   const __amdgpu_buffer_rsrc_t rv = tile_rsrc(c.vnext, c.vrem);
@@ -517,7 +512,7 @@ __device__ __forceinline__ void lds_issue(LdsCtx& c, unsigned char* Kd, unsigned
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)(Vd + (16 * c.w + 8 * i) * kRowBytes),
                                              16, c.vvo[i], 0, 0, 0);
   }
-  const int64_t kstep = kBN * c.k_sn * 2, vstep = kBN * c.v_sn * 2;
+  const int64_t kstep = kAdv * kBN * c.k_sn * 2, vstep = kAdv * kBN * c.v_sn * 2;
   c.knext += kstep;
   c.vnext += vstep;
   c.krem -= kstep;
@@ -543,23 +538,13 @@ __device__ __forceinline__ float max16(const f32x4 (&sc)[4]) {
   return max3_raw(max3_raw(a, b, d), max3_raw(e, f, sc[3][3]), kNegInf);
 }
 
-// One tile: wait for its loads, refill the stage of tile kt-1 with tile kt+2,
-// then scores, online softmax and PV from (Ks, Vs).
-template <bool kPaged>
-__device__ __forceinline__ void lds_step(LdsCtx& c, int kt, const unsigned char* Ks,
-                                         const unsigned char* Vs, unsigned char* Kn,
-                                         unsigned char* Vn) {
+// Scores, online softmax and PV of key tile kt from the LDS stage (Ks, Vs),
+// whose loads have landed; `refill` runs once the K operands are in
+// registers (the V^T reads come later).
+template <typename Refill>
+__device__ __forceinline__ void tile_compute(LdsCtx& c, int kt, const unsigned char* Ks,
+                                             const unsigned char* Vs, Refill&& refill) {
   const int key0 = kt * kBN;
-  // This wave's loads of tile kt have landed (the loads of tile kt+1 may stay
-  // in flight); after the barrier every wave's have, and every wave is done
-  // reading tile kt-1, whose stage is refilled with tile kt+2.  The barrier is
-  // bare (a workgroup fence would wait for all outstanding LDS loads); the
-  // signal fences keep the compiler from moving LDS accesses across it.
-  s_waitcnt_vm(kt + 1 < c.n_ktiles ? 4 : 0);
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_barrier();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-
   // K operands of tile kt, then (in flight under the score MFMAs and the
   // softmax) its V^T operands.
   const unsigned ks = lds_addr(Ks), vs = lds_addr(Vs);
@@ -592,7 +577,7 @@ __device__ __forceinline__ void lds_step(LdsCtx& c, int kt, const unsigned char*
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) ka[ch][j][kk] = __builtin_bit_cast(f16x8, kr[ch][j][kk]);
   // Refill after the K operands are in registers (the V^T reads come later).
-  if (kt + 2 < c.n_ktiles) lds_issue<kPaged>(c, Kn, Vn);  // tile kt + 2
+  refill();
   f32x4 sc[4];
 #pragma unroll
   for (int ch = 0; ch < 2; ++ch)
@@ -652,51 +637,45 @@ __device__ __forceinline__ void lds_step(LdsCtx& c, int kt, const unsigned char*
     }
 }
 
-template <bool kRopeQ, bool kPaged>
-__global__ __launch_bounds__(kWaves * 64) void prefill_lds_kernel(Args a) {
-  // Three stages, each its own K and V array so that loads into one stage are
-  // visibly disjoint from reads of another (no conservative waits).
-  __shared__ __attribute__((aligned(16))) unsigned char k0[kBN * kRowBytes], v0[kBN * kRowBytes];
-  __shared__ __attribute__((aligned(16))) unsigned char k1[kBN * kRowBytes], v1[kBN * kRowBytes];
-  __shared__ __attribute__((aligned(16))) unsigned char k2[kBN * kRowBytes], v2[kBN * kRowBytes];
+// Two-group form, for prompts whose query tiles all fit on the chip at once
+// (two workgroups per CU): one workgroup of eight waves per query tile.
+// Waves 0-3 take its even key tiles and waves 4-7 its odd ones, each group a
+// copy of the four-wave pipeline above (16 query rows per wave, the same
+// tile_compute), on a two-stage LDS ring that holds both groups' tiles: the
+// loads of step i + 1 are issued after step i's barrier, when every wave is
+// done with step i - 1's stage.  At the end the odd group's softmax states
+// merge into the even group's through LDS.  The heaviest query tile takes
+// half as many steps, with no partial or merge through memory.
+constexpr int kWaves2 = 8;
+constexpr int kTileBytes = kBN * kRowBytes;
 
-  // One-dimensional grid, (work item, b * QH + q head) with the head
-  // fastest, so that the dispatcher hands out the heaviest items of every
-  // head first (a 2-D grid walks all items of head 0 before any of head 1,
-  // and the last head's heaviest items would start last).  Work item ->
-  // (query tile, part), heaviest query tiles first, the parts of one query
-  // tile consecutive.
+template <bool kRopeQ, bool kPaged>
+__global__ __launch_bounds__(kWaves2 * 64, 4) void prefill_lds2_kernel(Args a) {
+  __shared__ __attribute__((aligned(16))) unsigned char ring[2][2][2][kTileBytes];  // [stage][group][K, V]
+
+  // One-dimensional grid, (query tile, b * QH + q head) with the head
+  // fastest and the heaviest query tiles first.
   const int n_bq = a.B * a.QH;
-  const int item = (int)(blockIdx.x / n_bq);
   const int n_mtiles = (a.S + kBM - 1) / kBM;
-  int mt = n_mtiles - 1 - item, part = 0, n_parts = 1;
-  if (a.split_tiles > 0) {
-    // Query tiles [g*T, g*T + T) have g + 1 parts each; walk the groups from
-    // the top (the top group may be partial).
-    const int T = a.split_tiles;
-    int rem = item, hi = n_mtiles - 1;
-    for (;;) {
-      const int g = hi / T, np = g + 1, cnt = hi - g * T + 1;
-      if (rem < cnt * np || g == 0) {
-        mt = hi - rem / np;
-        part = rem % np;
-        n_parts = np;
-        break;
-      }
-      rem -= cnt * np;
-      hi = g * T - 1;
-    }
-  }
+  const int mt = n_mtiles - 1 - (int)(blockIdx.x / n_bq);
   const int bq = (int)(blockIdx.x % n_bq);
   const int b = bq / a.QH, hq = bq % a.QH;
   const int hk = hq / a.G;
   const int tid = threadIdx.x;
-  const int lane = tid & 63, w = tid >> 6;
+  // Wave-uniform (scalar) group and row block: the group picks the tiles'
+  // addresses, which buffer resources need in scalar registers.
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = wave >> 2;  // key tiles g, g + 2, ...
+  const int w = wave & 3;   // 16-row block of the query tile
   const int col = lane & 15, grp = lane >> 4;
   int S;
   int64_t tok0;
   row_span(a, b, S, tok0);
   if (mt * kBM >= S) return;  // a shorter packed row: this query tile is empty
+  const int key_end = (mt + 1) * kBM < S ? (mt + 1) * kBM : S;
+  const int n_all = (key_end + kBN - 1) / kBN;
+  const int n_steps = (n_all + 1) / 2;
+  const int n_mine = (n_all - g + 1) / 2;
 
   LdsCtx c;
   const int64_t kvt = a.kv_packed ? tok0 : 0;
@@ -708,12 +687,7 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_lds_kernel(Args a) {
   c.mt = mt;
   c.grp = grp;
   c.w = w;
-  const int key_end = (mt + 1) * kBM < S ? (mt + 1) * kBM : S;
-  const int n_all = (key_end + kBN - 1) / kBN;
-  const int kt0 = part * n_all / n_parts;       // this part's key tiles [kt0, end)
-  c.n_ktiles = (part + 1) * n_all / n_parts;
   c.qrow = mt * kBM + w * 16 + col;
-  // Loader mapping: lane -> row 8i + lane/8 of the wave's 16, physical chunk lane % 8.
   c.lrow0 = 16 * w + (lane >> 3);
   c.pch = lane & 7;
 #pragma unroll
@@ -739,10 +713,10 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_lds_kernel(Args a) {
       qcs[3] = load16(a.sin + co + 32);
     }
   }
-  c.knext = reinterpret_cast<const unsigned char*>(c.kb + (int64_t)kt0 * kBN * c.k_sn);
-  c.vnext = reinterpret_cast<const unsigned char*>(c.vb + (int64_t)kt0 * kBN * c.v_sn);
-  c.krem = (int64_t)(S - kt0 * kBN) * c.k_sn * 2;
-  c.vrem = (int64_t)(S - kt0 * kBN) * c.v_sn * 2;
+  c.knext = reinterpret_cast<const unsigned char*>(c.kb + (int64_t)g * kBN * c.k_sn);
+  c.vnext = reinterpret_cast<const unsigned char*>(c.vb + (int64_t)g * kBN * c.v_sn);
+  c.krem = (int64_t)(S - g * kBN) * c.k_sn * 2;
+  c.vrem = (int64_t)(S - g * kBN) * c.v_sn * 2;
   if (kPaged) {
     c.kpool = reinterpret_cast<const unsigned char*>(a.k + hk * a.k_sh);
     c.vpool = reinterpret_cast<const unsigned char*>(a.v + hk * a.v_sh);
@@ -753,17 +727,12 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_lds_kernel(Args a) {
     c.log2p = a.log2p;
     c.ppr = a.ppr;
     c.n_pages = a.n_pages;
-    c.kt_issue = kt0;
-    load_pids(c, (int)((a.start_pos + (int64_t)kt0 * kBN) >> a.log2p));
+    c.kt_issue = g;
+    load_pids(c, (int)((a.start_pos + (int64_t)g * kBN) >> a.log2p));
   }
-  lds_issue<kPaged>(c, k0, v0);                            // tile kt0
-  if (kt0 + 1 < c.n_ktiles) lds_issue<kPaged>(c, k1, v1);  // tile kt0 + 1
+  if (n_mine > 0) lds_issue<kPaged, 2>(c, ring[0][g][0], ring[0][g][1]);  // tile g
   if (kRopeQ) rope_pair(c.qf[0], c.qf[1], qcs[0], qcs[1], qcs[2], qcs[3]);
-
   {
-    // K operand row r = 32 ch + 8 (col / 4) + 4 j + col % 4 and V^T row
-    // r = 32 ch + 8 grp + 4 h + col / 4: ch and j / h set bits 5 and 2 of r,
-    // which the swizzle (bits 1, 3, 4) does not read.
     const int rk = 8 * (col >> 2) + (col & 3);
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) c.koff[kk] = rk * kRowBytes + 16 * ((grp + 4 * kk) ^ swz(rk));
@@ -780,178 +749,58 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_lds_kernel(Args a) {
 #pragma unroll
   for (int t = 0; t < 4; ++t) c.o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int kt = kt0; kt < c.n_ktiles; kt += kStages) {
-    lds_step<kPaged>(c, kt, k0, v0, k2, v2);
-    if (kt + 1 < c.n_ktiles) lds_step<kPaged>(c, kt + 1, k1, v1, k0, v0);
-    if (kt + 2 < c.n_ktiles) lds_step<kPaged>(c, kt + 2, k2, v2, k1, v1);
+  for (int i = 0; i < n_steps; ++i) {
+    // This wave's loads of step i have landed; after the barrier every
+    // wave's have, and every wave is done with step i - 1's stage, which
+    // takes step i + 1's tiles.  (A group without a tile in the last step
+    // still takes part in the barrier.)
+    s_waitcnt_vm(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    if (i < n_mine) {
+      const int st = i & 1;
+      tile_compute(c, 2 * i + g, ring[st][g][0], ring[st][g][1], [&] {
+        if (i + 1 < n_mine) lds_issue<kPaged, 2>(c, ring[st ^ 1][g][0], ring[st ^ 1][g][1]);
+      });
+    }
   }
 
+  // Merge the groups: the odd group's (o, m, l) through LDS (the ring is
+  // free once every wave is past its last step).
   float l_run = c.l4[0];
-  if (n_parts > 1) {
-    // Partial of a split query tile: unnormalised o, running max (log2
-    // units) and sum.  Layout [bq][mt][part][row][kPartVals]; grp 0 also
-    // writes m and l.
-    const int row = w * 16 + col;
-    float* tile_parts = a.part + ((int64_t)bq * n_mtiles + mt) * a.max_parts * kBM * kPartVals;
-    if (a.ticket == nullptr) {  // merged by prefill_merge_kernel
-      float* pp = tile_parts + ((int64_t)part * kBM + row) * kPartVals;
+  f32x4* sm_o = reinterpret_cast<f32x4*>(&ring[0][0][0][0]);          // [w][t][lane]
+  float* sm_ml = reinterpret_cast<float*>(&ring[1][0][0][0]);          // [w][lane][m, l]
+  __syncthreads();
+  if (g == 1) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) *reinterpret_cast<f32x4*>(pp + 16 * t + 4 * grp) = c.o[t];
-      if (grp == 0) {
-        pp[64] = c.m_use;
-        pp[65] = l_run;
-      }
-      return;
-    }
-    // Single launch: write-through (sc1) stores, wait for them, take the
-    // query tile's ticket; the part that completes the count merges every
-    // part (the others' partials through sc1 loads, its own from registers)
-    // and re-arms the ticket.
-    __shared__ int sh_last;
-    const __amdgpu_buffer_rsrc_t rp =
-        buffer_rsrc(tile_parts, (int64_t)a.max_parts * kBM * kPartVals * 4);
-    const int own = (part * kBM + row) * kPartVals;
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, c.o[t]), rp,
-                                             (own + 16 * t + 4 * grp) * 4, 0, kSc1);
-    if (grp == 0) {
-      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, c.m_use), rp,
-                                            (own + 64) * 4, 0, kSc1);
-      __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, l_run), rp,
-                                            (own + 65) * 4, 0, kSc1);
-    }
-    int* tk = a.ticket + (int64_t)bq * n_mtiles + mt;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __syncthreads();
-    if (tid == 0) sh_last = atomicAdd(tk, 1) == n_parts - 1;
-    __syncthreads();
-    if (!sh_last) return;
-    // Fold the other parts into (m_use, l_run, o), four parts per batch with
-    // all their loads issued first.
-    for (int p0 = 0; p0 < n_parts; p0 += 4) {
-      f32x4 po[4][4];
-      float pm[4], pl[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int p = p0 + u;
-        const int off = (p * kBM + row) * kPartVals;  // past the tile's slots: reads 0
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-          po[u][t] = __builtin_bit_cast(
-              f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, (off + 16 * t + 4 * grp) * 4, 0, kSc1));
-        pm[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, (off + 64) * 4, 0, kSc1));
-        pl[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rp, (off + 65) * 4, 0, kSc1));
-      }
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int p = p0 + u;
-        if (p >= n_parts || p == part) continue;
-        const float mn = fmaxf(c.m_use, pm[u]);
-        const float s_old = (c.m_use == kNegInf) ? 0.f : fast_exp2(c.m_use - mn);
-        const float s_new = (pm[u] == kNegInf) ? 0.f : fast_exp2(pm[u] - mn);
-        l_run = l_run * s_old + pl[u] * s_new;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) c.o[t] = c.o[t] * s_old + po[u][t] * s_new;
-        c.m_use = mn;
-      }
-    }
-    if (tid == 0) __hip_atomic_store(tk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int t = 0; t < 4; ++t) sm_o[(w * 4 + t) * 64 + lane] = c.o[t];
+    sm_ml[(w * 64 + lane) * 2] = c.m_use;
+    sm_ml[(w * 64 + lane) * 2 + 1] = l_run;
   }
-  if (c.qrow < S) {
-    const float inv = 1.f / l_run;
-    f16* op = a.out + b * a.o_sb + hq * a.o_sh + (tok0 + c.qrow) * a.o_sn;
+  __syncthreads();
+  if (g == 1 || c.qrow >= S) return;
+  const float m1 = sm_ml[(w * 64 + lane) * 2], l1 = sm_ml[(w * 64 + lane) * 2 + 1];
+  const float mn = fmaxf(c.m_use, m1);
+  const float s0 = (c.m_use == kNegInf) ? 0.f : fast_exp2(c.m_use - mn);
+  const float s1 = (m1 == kNegInf) ? 0.f : fast_exp2(m1 - mn);
+  const float inv = 1.f / (l_run * s0 + l1 * s1);
+  f16* op = a.out + b * a.o_sb + hq * a.o_sh + (tok0 + c.qrow) * a.o_sn;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      f16x4 r;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) r[i] = (f16)(c.o[t][i] * inv);
-      *reinterpret_cast<f16x4*>(op + 16 * t + 4 * grp) = r;
-    }
-  }
-}
-
-// One merged (row, 4 dims) item: o = (o0 s0 + o1 s1) / (l0 s0 + l1 s1) with
-// s_i = 2^(m_i - max(m0, m1)), rounded once to fp16.
-__device__ __forceinline__ void merge_write(const Args& a, int b, int hq, int qrow, int d4,
-                                            f32x4 o0, float m0, float l0, f32x4 o1, float m1,
-                                            float l1) {
-  const float m = fmaxf(m0, m1);
-  const float s0 = (m0 == kNegInf) ? 0.f : fast_exp2(m0 - m);
-  const float s1 = (m1 == kNegInf) ? 0.f : fast_exp2(m1 - m);
-  const float inv = 1.f / (l0 * s0 + l1 * s1);
-  const f32x4 o = o0 * s0 + o1 * s1;
-  f16x4 r;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) r[i] = (f16)(o[i] * inv);
-  *reinterpret_cast<f16x4*>(a.out + b * a.o_sb + hq * a.o_sh + (int64_t)qrow * a.o_sn + 4 * d4) = r;
-}
-
-// Merge of the P partials of each split query tile: grid (query tiles that
-// split, B*QH), four (row, 4 dims) items per thread, each part's loads
-// issued together.  o = sum_p o_p s_p / sum_p l_p s_p with s_p = 2^(m_p - m),
-// m = max_p m_p, rounded once to fp16.
-__global__ __launch_bounds__(256) void prefill_merge_kernel(Args a) {
-  const int n_mtiles = (a.S + kBM - 1) / kBM;
-  const int mt = a.split_tiles + blockIdx.x;  // the first split query tile is split_tiles
-  const int bq = blockIdx.y;
-  const int b = bq / a.QH, hq = bq % a.QH;
-  const int n_parts = (mt + a.split_tiles) / a.split_tiles;
-  const float* p0 = a.part + ((int64_t)bq * n_mtiles + mt) * a.max_parts * kBM * kPartVals;
-  constexpr int kItems = kBM * 16 / 256;
-  float M[kItems], L[kItems];
-  f32x4 O[kItems];
-#pragma unroll
-  for (int i = 0; i < kItems; ++i) {
-    M[i] = kNegInf;
-    L[i] = 0.f;
-    O[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
-  for (int p = 0; p < n_parts; ++p) {
-    const float* pp = p0 + (int64_t)p * kBM * kPartVals;
-    f32x4 o[kItems];
-    float m[kItems], l[kItems];
-#pragma unroll
-    for (int i = 0; i < kItems; ++i) {
-      const int it = threadIdx.x + 256 * i;
-      const int row = it >> 4, d4 = it & 15;
-      o[i] = *reinterpret_cast<const f32x4*>(pp + row * kPartVals + 4 * d4);
-      m[i] = pp[row * kPartVals + 64];
-      l[i] = pp[row * kPartVals + 65];
-    }
-#pragma unroll
-    for (int i = 0; i < kItems; ++i) {
-      const float mn = fmaxf(M[i], m[i]);
-      const float s_old = (M[i] == kNegInf) ? 0.f : fast_exp2(M[i] - mn);
-      const float s_new = (m[i] == kNegInf) ? 0.f : fast_exp2(m[i] - mn);
-      L[i] = L[i] * s_old + l[i] * s_new;
-      O[i] = O[i] * s_old + o[i] * s_new;
-      M[i] = mn;
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < kItems; ++i) {
-    const int it = threadIdx.x + 256 * i;
-    const int qrow = mt * kBM + (it >> 4), d4 = it & 15;
-    if (qrow >= a.S) continue;
-    const float inv = 1.f / L[i];
+  for (int t = 0; t < 4; ++t) {
+    const f32x4 o = c.o[t] * s0 + sm_o[(w * 4 + t) * 64 + lane] * s1;
     f16x4 r;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) r[c] = (f16)(O[i][c] * inv);
-    *reinterpret_cast<f16x4*>(a.out + b * a.o_sb + hq * a.o_sh + (int64_t)qrow * a.o_sn + 4 * d4) = r;
+    for (int i = 0; i < 4; ++i) r[i] = (f16)(o[i] * inv);
+    *reinterpret_cast<f16x4*>(op + 16 * t + 4 * grp) = r;
   }
 }
 
-// Pre-pass of the fused op: rotated K and raw V of every token into the cache
-// at slots start_pos + i (bit-exact eager rounding), so the attention kernel
-// streams finished rows.  Block = 16 tokens x (4 K chunk pairs + 8 V chunks).
+// Pre-pass of the cached prefill: rotated K (or K as is) and raw V of every
+// token into the cache at slot start_pos + token, once per (b, kv head);
+// 16 tokens per workgroup, 16 threads per token (4 for K's rotate-half chunk
+// pairs, 8 for V's chunks).
 __global__ __launch_bounds__(256) void rope_kv_prefill_kernel(Args a) {
-  if (a.ticket != nullptr) {
-    // Arm the attention kernel's merge tickets (one per [bq][query tile]).
-    const int n = a.B * a.QH * ((a.S + kBM - 1) / kBM);
-    const int gid = (blockIdx.y * gridDim.x + blockIdx.x) * 256 + threadIdx.x;
-    for (int i = gid; i < n; i += gridDim.x * gridDim.y * 256) a.ticket[i] = 0;
-  }
   const int tok = blockIdx.x * 16 + (threadIdx.x >> 4);
   const int sub = threadIdx.x & 15;
   const int bh = blockIdx.y;
@@ -991,56 +840,6 @@ using namespace qf;
 
 static bool aligned16p(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Key tiles per split part: query tiles with more key tiles than this run as
-// several workgroups.  Short prompts (fewer query tiles) are not split.
-#ifndef QF_PF_SPLIT_TILES
-#define QF_PF_SPLIT_TILES 16
-#endif
-static constexpr int kSplitTiles = QF_PF_SPLIT_TILES;
-
-static void split_plan(int S, int& split_tiles, int& max_parts, int& n_items, int& n_merge) {
-  const int n_mtiles = (S + qf::prefill::kBM - 1) / qf::prefill::kBM;
-  split_tiles = 0;
-  max_parts = 1;
-  n_items = n_mtiles;
-  n_merge = 0;
-  if (n_mtiles <= kSplitTiles) return;
-  split_tiles = kSplitTiles;
-  max_parts = (n_mtiles + kSplitTiles - 1) / kSplitTiles;
-  n_items = 0;
-  for (int mt = 0; mt < n_mtiles; ++mt) n_items += (mt + kSplitTiles) / kSplitTiles;
-  n_merge = n_mtiles - kSplitTiles;
-}
-
-extern "C" int64_t qf_prefill_workspace_bytes(int B, int QH, int S) {
-  using namespace qf::prefill;
-  if (B < 1 || QH < 1 || S < 1) return 0;
-  int split_tiles, max_parts, n_items, n_merge;
-  split_plan(S, split_tiles, max_parts, n_items, n_merge);
-  if (n_merge == 0) return 0;
-  const int n_mtiles = (S + kBM - 1) / kBM;
-  // fp32 partials [B*QH][query tile][part][row][kPartVals], then one int32
-  // merge ticket per [B*QH][query tile].
-  return (int64_t)B * QH * n_mtiles * max_parts * kBM * kPartVals * (int64_t)sizeof(float) +
-         (int64_t)B * QH * n_mtiles * (int64_t)sizeof(int);
-}
-
-extern "C" int qf_prefill_attn(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sn,
-                               const void* k, int64_t k_sb, int64_t k_sh, int64_t k_sn,
-                               const void* v, int64_t v_sb, int64_t v_sh, int64_t v_sn,
-                               const void* cos, const void* sin, int64_t cs_sb, int64_t cs_sn,
-                               void* k_cache, int64_t kc_sb, int64_t kc_sh, int64_t kc_sn,
-                               void* v_cache, int64_t vc_sb, int64_t vc_sh, int64_t vc_sn,
-                               int64_t start_pos, int cap,
-                               void* out, int64_t o_sb, int64_t o_sh, int64_t o_sn,
-                               int B, int QH, int KVH, int S, int D, float scale,
-                               void* stream) {
-  return qf_prefill_attn_ws(q, q_sb, q_sh, q_sn, k, k_sb, k_sh, k_sn, v, v_sb, v_sh, v_sn, cos,
-                            sin, cs_sb, cs_sn, k_cache, kc_sb, kc_sh, kc_sn, v_cache, vc_sb, vc_sh,
-                            vc_sn, start_pos, cap, out, o_sb, o_sh, o_sn, B, QH, KVH, S, D, scale,
-                            nullptr, 0, stream);
-}
-
 using qf::prefill::Args;
 
 // Shared launch sequence of the dense and the packed (varlen) entry points;
@@ -1076,22 +875,16 @@ static int prefill_launch(Args a, bool rope, bool append, hipStream_t st) {
   } else if (paged) {
     return QF_ERR_INVALID_ARG;  // paged prefill always appends
   }
-  int n_items = grid.x, n_merge = 0;
-  if (a.split_tiles > 0) {
-    int st_, mp_;
-    split_plan(S, st_, mp_, n_items, n_merge);
-  }
-  if ((int64_t)n_items * B * QH > 0x7fffffff) return QF_ERR_UNSUPPORTED;
-  const dim3 lgrid((unsigned)(n_items * B * QH));
+  // One eight-wave workgroup per (query tile, b * QH + q head).
+  if ((int64_t)grid.x * B * QH > 0x7fffffff) return QF_ERR_UNSUPPORTED;
+  const dim3 lgrid((unsigned)(grid.x * B * QH)), lblock(kWaves2 * 64);
   if (paged) {
-    if (rope) hipLaunchKernelGGL((prefill_lds_kernel<true, true>), lgrid, block, 0, st, a);
-    else hipLaunchKernelGGL((prefill_lds_kernel<false, true>), lgrid, block, 0, st, a);
+    if (rope) hipLaunchKernelGGL((prefill_lds2_kernel<true, true>), lgrid, lblock, 0, st, a);
+    else hipLaunchKernelGGL((prefill_lds2_kernel<false, true>), lgrid, lblock, 0, st, a);
   } else {
-    if (rope) hipLaunchKernelGGL((prefill_lds_kernel<true, false>), lgrid, block, 0, st, a);
-    else hipLaunchKernelGGL((prefill_lds_kernel<false, false>), lgrid, block, 0, st, a);
+    if (rope) hipLaunchKernelGGL((prefill_lds2_kernel<true, false>), lgrid, lblock, 0, st, a);
+    else hipLaunchKernelGGL((prefill_lds2_kernel<false, false>), lgrid, lblock, 0, st, a);
   }
-  if (n_merge > 0 && a.ticket == nullptr)
-    hipLaunchKernelGGL(prefill_merge_kernel, dim3(n_merge, B * QH), dim3(256), 0, st, a);
   return (int)hipGetLastError();
 }
 
@@ -1129,10 +922,6 @@ static int fill_common(Args& a, const void* q, const void* k, const void* v, con
   a.out = static_cast<f16*>(out);
   a.B = B; a.QH = QH; a.KVH = KVH; a.G = QH / KVH; a.S = S;
   a.scale_log2 = scale * kLog2e;
-  a.part = nullptr;
-  a.split_tiles = 0;
-  a.max_parts = 1;
-  a.ticket = nullptr;
   a.cu = nullptr;
   a.total = 0;
   a.kv_packed = 1;
@@ -1144,16 +933,16 @@ static int fill_common(Args& a, const void* q, const void* k, const void* v, con
   return QF_OK;
 }
 
-extern "C" int qf_prefill_attn_ws(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sn,
-                                  const void* k, int64_t k_sb, int64_t k_sh, int64_t k_sn,
-                                  const void* v, int64_t v_sb, int64_t v_sh, int64_t v_sn,
-                                  const void* cos, const void* sin, int64_t cs_sb, int64_t cs_sn,
-                                  void* k_cache, int64_t kc_sb, int64_t kc_sh, int64_t kc_sn,
-                                  void* v_cache, int64_t vc_sb, int64_t vc_sh, int64_t vc_sn,
-                                  int64_t start_pos, int cap,
-                                  void* out, int64_t o_sb, int64_t o_sh, int64_t o_sn,
-                                  int B, int QH, int KVH, int S, int D, float scale,
-                                  void* workspace, int64_t workspace_bytes, void* stream) {
+extern "C" int qf_prefill_attn(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sn,
+                               const void* k, int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                               const void* v, int64_t v_sb, int64_t v_sh, int64_t v_sn,
+                               const void* cos, const void* sin, int64_t cs_sb, int64_t cs_sn,
+                               void* k_cache, int64_t kc_sb, int64_t kc_sh, int64_t kc_sn,
+                               void* v_cache, int64_t vc_sb, int64_t vc_sh, int64_t vc_sn,
+                               int64_t start_pos, int cap,
+                               void* out, int64_t o_sb, int64_t o_sh, int64_t o_sn,
+                               int B, int QH, int KVH, int S, int D, float scale,
+                               void* stream) {
   using namespace qf::prefill;
   Args a;
   bool rope, append;
@@ -1169,18 +958,6 @@ extern "C" int qf_prefill_attn_ws(const void* q, int64_t q_sb, int64_t q_sh, int
   a.v_sb = v_sb; a.v_sh = v_sh; a.v_sn = v_sn;
   a.cs_sb = cs_sb; a.cs_sn = cs_sn;
   a.o_sb = o_sb; a.o_sh = o_sh; a.o_sn = o_sn;
-  if (workspace != nullptr && workspace_bytes > 0) {
-    if (!aligned16p(workspace) || workspace_bytes < qf_prefill_workspace_bytes(B, QH, S))
-      return QF_ERR_INVALID_ARG;
-    a.part = static_cast<float*>(workspace);
-    int n_items, n_merge;
-    split_plan(S, a.split_tiles, a.max_parts, n_items, n_merge);
-    // With a pre-pass (cache append) to arm them, the tickets let the last
-    // part of each split query tile merge in the attention kernel itself.
-    if (append && n_merge > 0)
-      a.ticket = reinterpret_cast<int*>(a.part + (int64_t)B * QH * ((S + kBM - 1) / kBM) *
-                                                     a.max_parts * kBM * kPartVals);
-  }
   return prefill_launch(a, rope, append, static_cast<hipStream_t>(stream));
 }
 

@@ -371,13 +371,8 @@ def _prefill_launch(query, key, value, out, cos=None, sin=None, key_cache=None,
     kc_s = key_cache.stride()[:3] if key_cache is not None else (0, 0, 0)
     vc_s = value_cache.stride()[:3] if value_cache is not None else (0, 0, 0)
     lib = _lib.load()
-    # Workspace for the split of the heaviest query tiles (the streaming
-    # kernel runs unless RoPE is requested without a cache to hold rotated K).
-    ws_bytes = 0 if (cos is not None and key_cache is None) else \
-        int(lib.qf_prefill_workspace_bytes(b, qh, s))
-    ws = torch.empty(ws_bytes, device=query.device, dtype=torch.uint8) if ws_bytes else None
     with torch.cuda.device(query.device):
-        rc = lib.qf_prefill_attn_ws(
+        rc = lib.qf_prefill_attn(
             query.data_ptr(), *query.stride()[:3],
             key.data_ptr(), *key.stride()[:3],
             value.data_ptr(), *value.stride()[:3],
@@ -387,8 +382,8 @@ def _prefill_launch(query, key, value, out, cos=None, sin=None, key_cache=None,
             int(start_pos), cap,
             out.data_ptr(), *out.stride()[:3],
             b, qh, kvh, s, d, float(d ** -0.5),
-            _ptr(ws), ws_bytes, _stream(query.device))
-    _lib.check(rc, "qf_prefill_attn_ws")
+            _stream(query.device))
+    _lib.check(rc, "qf_prefill_attn")
     return out
 
 

@@ -1,10 +1,10 @@
 """Seeded sweep of causal-prefill shapes against the CPU oracle.
 
-Each case draws batch, head layout (query heads per kv head), prompt length,
-the entry point (plain op, or RoPE + cache append at an offset) from one
-seed; prompts longer than 1024 tokens take the split-query-tile paths (the
-separate merge launch for the plain op, the in-kernel ticket merge for the
-fused one).  Oracle: ``oracle.causal_prefill`` on ``oracle.apply_rope_fp16``
+Each case draws batch, head layout (query heads per kv head), prompt length
+(1 to 2100 tokens: 1 to 33 query tiles, whose two halves of waves take
+their key tiles alternately, one half idle in the last step of every odd
+count) and the entry point (plain op, or RoPE + cache append at an offset)
+from one seed.  Oracle: ``oracle.causal_prefill`` on ``oracle.apply_rope_fp16``
 rotated q/k (SE:164-251, SE:542-554).  Attention within max-abs-err 2e-3,
 cache rows bit-exact.
 """
