@@ -637,21 +637,20 @@ __device__ __forceinline__ void tile_compute(LdsCtx& c, int kt, const unsigned c
     }
 }
 
-// Two-group form, for prompts whose query tiles all fit on the chip at once
-// (two workgroups per CU): one workgroup of eight waves per query tile.
-// Waves 0-3 take its even key tiles and waves 4-7 its odd ones, each group a
-// copy of the four-wave pipeline above (16 query rows per wave, the same
-// tile_compute), on a two-stage LDS ring that holds both groups' tiles: the
-// loads of step i + 1 are issued after step i's barrier, when every wave is
-// done with step i - 1's stage.  At the end the odd group's softmax states
-// merge into the even group's through LDS.  The heaviest query tile takes
-// half as many steps, with no partial or merge through memory.
-constexpr int kWaves2 = 8;
+// Grouped form: one workgroup of 4 kG waves per query tile.  Wave group g
+// (waves 4g .. 4g + 3) takes key tiles g, g + kG, ..., each group a copy of
+// the four-wave pipeline (16 query rows per wave, the same tile_compute), on
+// a two-stage LDS ring that holds every group's tile of a step: the loads of
+// step i + 1 are issued after step i's barrier, when every wave is done with
+// step i - 1's stage.  At the end groups 1 .. kG-1 hand their softmax states
+// to group 0 through LDS, which merges them.  The heaviest query tile takes
+// 1/kG of the steps, with no partial or merge through memory.  kG = 2: two
+// workgroups per CU; kG = 4: one (both four waves per SIMD).
 constexpr int kTileBytes = kBN * kRowBytes;
 
-template <bool kRopeQ, bool kPaged>
-__global__ __launch_bounds__(kWaves2 * 64, 4) void prefill_lds2_kernel(Args a) {
-  __shared__ __attribute__((aligned(16))) unsigned char ring[2][2][2][kTileBytes];  // [stage][group][K, V]
+template <int kG, bool kRopeQ, bool kPaged>
+__global__ __launch_bounds__(kG * 4 * 64, 4) void prefill_lds2_kernel(Args a) {
+  __shared__ __attribute__((aligned(16))) unsigned char ring[2][kG][2][kTileBytes];  // [stage][group][K, V]
 
   // One-dimensional grid, (query tile, b * QH + q head) with the head
   // fastest and the heaviest query tiles first.
@@ -665,7 +664,7 @@ __global__ __launch_bounds__(kWaves2 * 64, 4) void prefill_lds2_kernel(Args a) {
   // Wave-uniform (scalar) group and row block: the group picks the tiles'
   // addresses, which buffer resources need in scalar registers.
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int g = wave >> 2;  // key tiles g, g + 2, ...
+  const int g = wave >> 2;  // key tiles g, g + kG, ...
   const int w = wave & 3;   // 16-row block of the query tile
   const int col = lane & 15, grp = lane >> 4;
   int S;
@@ -674,8 +673,8 @@ __global__ __launch_bounds__(kWaves2 * 64, 4) void prefill_lds2_kernel(Args a) {
   if (mt * kBM >= S) return;  // a shorter packed row: this query tile is empty
   const int key_end = (mt + 1) * kBM < S ? (mt + 1) * kBM : S;
   const int n_all = (key_end + kBN - 1) / kBN;
-  const int n_steps = (n_all + 1) / 2;
-  const int n_mine = (n_all - g + 1) / 2;
+  const int n_steps = (n_all + kG - 1) / kG;
+  const int n_mine = (n_all - g + kG - 1) / kG;
 
   LdsCtx c;
   const int64_t kvt = a.kv_packed ? tok0 : 0;
@@ -730,7 +729,7 @@ __global__ __launch_bounds__(kWaves2 * 64, 4) void prefill_lds2_kernel(Args a) {
     c.kt_issue = g;
     load_pids(c, (int)((a.start_pos + (int64_t)g * kBN) >> a.log2p));
   }
-  if (n_mine > 0) lds_issue<kPaged, 2>(c, ring[0][g][0], ring[0][g][1]);  // tile g
+  if (n_mine > 0) lds_issue<kPaged, kG>(c, ring[0][g][0], ring[0][g][1]);  // tile g
   if (kRopeQ) rope_pair(c.qf[0], c.qf[1], qcs[0], qcs[1], qcs[2], qcs[3]);
   {
     const int rk = 8 * (col >> 2) + (col & 3);
@@ -760,35 +759,51 @@ __global__ __launch_bounds__(kWaves2 * 64, 4) void prefill_lds2_kernel(Args a) {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     if (i < n_mine) {
       const int st = i & 1;
-      tile_compute(c, 2 * i + g, ring[st][g][0], ring[st][g][1], [&] {
-        if (i + 1 < n_mine) lds_issue<kPaged, 2>(c, ring[st ^ 1][g][0], ring[st ^ 1][g][1]);
+      tile_compute(c, kG * i + g, ring[st][g][0], ring[st][g][1], [&] {
+        if (i + 1 < n_mine) lds_issue<kPaged, kG>(c, ring[st ^ 1][g][0], ring[st ^ 1][g][1]);
       });
     }
   }
 
-  // Merge the groups: the odd group's (o, m, l) through LDS (the ring is
-  // free once every wave is past its last step).
+  // Merge the groups: groups 1 .. kG-1 write (o, m, l) to LDS (the ring is
+  // free once every wave is past its last step), group 0 merges them.
   float l_run = c.l4[0];
-  f32x4* sm_o = reinterpret_cast<f32x4*>(&ring[0][0][0][0]);          // [w][t][lane]
-  float* sm_ml = reinterpret_cast<float*>(&ring[1][0][0][0]);          // [w][lane][m, l]
+  f32x4* sm_o = reinterpret_cast<f32x4*>(&ring[0][0][0][0]);  // [g-1][w][t][lane]
+  float* sm_ml = reinterpret_cast<float*>(&ring[0][0][0][0] + (kG - 1) * 4 * 4 * 64 * 16);  // [g-1][w][lane][m, l]
   __syncthreads();
-  if (g == 1) {
+  if (g > 0) {
+    const int slot = (g - 1) * 4 + w;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) sm_o[(w * 4 + t) * 64 + lane] = c.o[t];
-    sm_ml[(w * 64 + lane) * 2] = c.m_use;
-    sm_ml[(w * 64 + lane) * 2 + 1] = l_run;
+    for (int t = 0; t < 4; ++t) sm_o[(slot * 4 + t) * 64 + lane] = c.o[t];
+    sm_ml[(slot * 64 + lane) * 2] = c.m_use;
+    sm_ml[(slot * 64 + lane) * 2 + 1] = l_run;
   }
   __syncthreads();
-  if (g == 1 || c.qrow >= S) return;
-  const float m1 = sm_ml[(w * 64 + lane) * 2], l1 = sm_ml[(w * 64 + lane) * 2 + 1];
-  const float mn = fmaxf(c.m_use, m1);
-  const float s0 = (c.m_use == kNegInf) ? 0.f : fast_exp2(c.m_use - mn);
-  const float s1 = (m1 == kNegInf) ? 0.f : fast_exp2(m1 - mn);
-  const float inv = 1.f / (l_run * s0 + l1 * s1);
+  if (g > 0 || c.qrow >= S) return;
+  float mg[kG], lg[kG];
+  mg[0] = c.m_use;
+  lg[0] = l_run;
+  float mn = c.m_use;
+#pragma unroll
+  for (int gg = 1; gg < kG; ++gg) {
+    const int slot = (gg - 1) * 4 + w;
+    mg[gg] = sm_ml[(slot * 64 + lane) * 2];
+    lg[gg] = sm_ml[(slot * 64 + lane) * 2 + 1];
+    mn = fmaxf(mn, mg[gg]);
+  }
+  float sg[kG], l_tot = 0.f;
+#pragma unroll
+  for (int gg = 0; gg < kG; ++gg) {
+    sg[gg] = (mg[gg] == kNegInf) ? 0.f : fast_exp2(mg[gg] - mn);
+    l_tot += lg[gg] * sg[gg];
+  }
+  const float inv = 1.f / l_tot;
   f16* op = a.out + b * a.o_sb + hq * a.o_sh + (tok0 + c.qrow) * a.o_sn;
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    const f32x4 o = c.o[t] * s0 + sm_o[(w * 4 + t) * 64 + lane] * s1;
+    f32x4 o = c.o[t] * sg[0];
+#pragma unroll
+    for (int gg = 1; gg < kG; ++gg) o += sm_o[((((gg - 1) * 4 + w) * 4) + t) * 64 + lane] * sg[gg];
     f16x4 r;
 #pragma unroll
     for (int i = 0; i < 4; ++i) r[i] = (f16)(o[i] * inv);
@@ -877,13 +892,17 @@ static int prefill_launch(Args a, bool rope, bool append, hipStream_t st) {
   }
   // One eight-wave workgroup per (query tile, b * QH + q head).
   if ((int64_t)grid.x * B * QH > 0x7fffffff) return QF_ERR_UNSUPPORTED;
-  const dim3 lgrid((unsigned)(grid.x * B * QH)), lblock(kWaves2 * 64);
+  const dim3 lgrid((unsigned)(grid.x * B * QH));
+  // Two groups (measured on MI355X: four, one 16-wave workgroup per CU,
+  // were slower at every size, 28.8 vs 26.0 us at S=2048).
+  constexpr int G = 2;
+  const dim3 lblock(G * 4 * 64);
   if (paged) {
-    if (rope) hipLaunchKernelGGL((prefill_lds2_kernel<true, true>), lgrid, lblock, 0, st, a);
-    else hipLaunchKernelGGL((prefill_lds2_kernel<false, true>), lgrid, lblock, 0, st, a);
+    if (rope) hipLaunchKernelGGL((prefill_lds2_kernel<G, true, true>), lgrid, lblock, 0, st, a);
+    else hipLaunchKernelGGL((prefill_lds2_kernel<G, false, true>), lgrid, lblock, 0, st, a);
   } else {
-    if (rope) hipLaunchKernelGGL((prefill_lds2_kernel<true, false>), lgrid, lblock, 0, st, a);
-    else hipLaunchKernelGGL((prefill_lds2_kernel<false, false>), lgrid, lblock, 0, st, a);
+    if (rope) hipLaunchKernelGGL((prefill_lds2_kernel<G, true, false>), lgrid, lblock, 0, st, a);
+    else hipLaunchKernelGGL((prefill_lds2_kernel<G, false, false>), lgrid, lblock, 0, st, a);
   }
   return (int)hipGetLastError();
 }
