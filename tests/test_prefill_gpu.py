@@ -196,3 +196,21 @@ def test_varlen_prefill_rope_append_matches_per_row_oracle(dev, lengths):
         assert torch.equal(vc[i, :, :n], v[sl].transpose(0, 1))
         assert torch.equal(kc[i, :, n:], kc0[i, :, n:])
         assert torch.equal(vc[i, :, n:], vc0[i, :, n:])
+
+
+@pytest.mark.parametrize("seq,batch", [(1, 1), (100, 2), (1100, 1)])
+def test_rope_without_cache(dev, seq, batch):
+    """RoPE on q and k with no cache to append to (the register-staged kernel
+    rotates each K tile on its way to LDS): matches the oracle on rotated
+    inputs."""
+    from qwenforge_amd import ops as ops_
+
+    case = workloads.prefill_case(seq, batch=batch, seed=50 + seq)
+    c = case.to(dev)
+    print(f"[prefill rope, no cache] S={seq} B={batch}", flush=True)
+    out = torch.empty_like(c.query)
+    ops_._prefill_launch(c.query, c.key, c.value, out, c.cos, c.sin)
+    torch.cuda.synchronize()
+    q_rot = oracle.apply_rope_fp16(case.query, case.cos, case.sin)
+    k_rot = oracle.apply_rope_fp16(case.key, case.cos, case.sin)
+    assert _err(out.cpu(), oracle.causal_prefill(q_rot, k_rot, case.value)) <= TOL
