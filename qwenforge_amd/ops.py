@@ -66,9 +66,11 @@ def choose_splits(batch: int, kv_heads: int, length: int, min_keys: int = 64,
     The (split, b, kv-head) workgroups fill the CUs once -- floor(CUs / pairs)
     splits -- or twice (two eight-wave workgroups share a CU) when that still
     allows the single-launch merge (<= 32 splits) and keeps splits at <= 512
-    keys; a count just above one per CU leaves a few CUs with a second
-    workgroup and costs up to 30% (measured: B=12 L=5760 at 11 splits, 264
-    workgroups, 16.7 us vs 13.1 us at 10).  Splits are never shorter than
+    keys; where one per CU fills every CU exactly, twice only with splits of
+    >= 256 keys, and never when one split per row already fills the chip (no
+    merge at all).  A count just above one per CU leaves a few CUs with a
+    second workgroup and costs up to 30% (measured: B=12 L=5760 at 11 splits,
+    264 workgroups, 16.7 us vs 13.1 us at 10).  Splits are never shorter than
     ``min_keys`` slots (twice that with 8 or more (b, kv head) pairs, where
     fewer, longer splits shorten the merge).  With at most 8 pairs and splits
     of >= 1024 keys the count doubles, so each wave keeps at most a few
@@ -84,7 +86,10 @@ def choose_splits(batch: int, kv_heads: int, length: int, min_keys: int = 64,
     by_len = max(1, math.ceil(length / (2 * min_keys if pairs >= 8 else min_keys)))
     s = max(1, target_workgroups // pairs)
     s2 = 2 * target_workgroups // pairs
-    if 1 < s2 <= 32 and length <= 512 * s2:
+    twice = 1 < s2 <= 32 and length <= 512 * s2
+    if twice and pairs * s == target_workgroups:
+        twice = s > 1 and length >= 256 * s2
+    if twice:
         s = s2
     if pairs <= 8 and length / s >= 1024:
         s *= 2

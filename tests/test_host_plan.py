@@ -20,6 +20,10 @@ from qwenforge_amd import ops
     (12, 5760, 21),    # the reference's benchmark shape: two per CU, fused
     (20, 4096, 12),
     (100, 4096, 1),    # 200 pairs: one split, no merge
+    (8, 4096, 16),     # one per CU fits exactly; twice would give 128-key splits
+    (16, 4096, 16),    # exact fit, but 256-key splits: twice
+    (32, 1024, 4),
+    (128, 1024, 1),    # 256 pairs: one split per row fills the chip, no merge
 ])
 def test_choose_splits_at_benchmark_shapes(batch, length, splits):
     assert ops.choose_splits(batch, 2, length) == splits
