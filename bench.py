@@ -316,15 +316,16 @@ def hbm_copy_ceiling(dev, mib=512, reps=20):
     return 2 * src.numel() * 2 / (ms * 1e-3) / 1e9
 
 
-def bench_prefill(steps, warmup, dev):
-    """Config 4: causal prefill S=2048 with fused RoPE + cache append."""
+def bench_prefill(steps, warmup, dev, seq=2048):
+    """Config 4: causal prefill S=2048 with fused RoPE + cache append (other
+    lengths for the long-prompt leg)."""
     import torch
 
     from qwenforge_amd import ops, workloads
 
-    case = workloads.prefill_case(2048, seed=0)
+    case = workloads.prefill_case(seq, seed=0)
     c = case.to(dev)
-    kc = torch.zeros(1, 2, 2048, 64, dtype=torch.float16, device=dev)
+    kc = torch.zeros(1, 2, seq, 64, dtype=torch.float16, device=dev)
     vc = torch.zeros_like(kc)
     per_graph = 8
 
@@ -592,6 +593,15 @@ def main():
             "us_per_layer": round(pf["us_per_layer"], 3),
             "TFLOPs": round(tf, 2),
             "mfma_frac": round(tf / FP16_MFMA_PEAK_TFLOPS, 4),
+        }
+        # The same prefill on a long prompt (same shape otherwise), where the
+        # causal imbalance between query tiles weighs less.
+        pl = bench_prefill(max(8, args.steps // 4), max(8, args.warmup // 2), dev, seq=8192)
+        tl = pl["flops"] / (pl["us_per_layer"] * 1e-6) / 1e12
+        line["prefill_long_s8192"] = {
+            "us_per_layer": round(pl["us_per_layer"], 3),
+            "TFLOPs": round(tl, 2),
+            "mfma_frac": round(tl / FP16_MFMA_PEAK_TFLOPS, 4),
         }
         e2e = bench_e2e(dev)
         line["decode_e2e_cfg5"] = {
