@@ -559,9 +559,6 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // (idle waves only lengthen the cross-wave merge).  The single-launch merge
 // gives each query a wave: NW >= G.
 static int pick_waves(const DecodeArgs& a, int mode) {
-#ifdef QF_DECODE_FORCE_NW
-  return QF_DECODE_FORCE_NW;
-#endif
   const int64_t wgs = (int64_t)a.splits * a.B * a.KVH;
   int nw = wgs <= 2 ? 16 : (wgs <= 512 ? 8 : 4);
   const int split_len = (a.cap + a.splits - 1) / a.splits;
