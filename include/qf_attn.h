@@ -73,12 +73,14 @@ int qf_abi_version(void);
  *          sum p).  Split s covers [s*split_len, min(+split_len, upper)) with
  *          split_len = ceil(upper / S) rounded up to a multiple of 32.
  *   ticket NULL: the merge runs as a second kernel (reference two-launch
- *          shape).  Non-NULL: int32[B*KVH*(ceil(splits/16)+1)], zero-filled
- *          once by the caller; the merge runs inside the same launch (the last
- *          workgroup of each group of 16 splits merges its group, the last of
- *          those produces the output) and every counter is re-armed to 0, so
- *          the same ticket serves every later call with the same split count.
- *          Calls that share a ticket must not overlap in time.
+ *          shape).  Non-NULL: int32[B*KVH], one counter per (b, kv head),
+ *          zero-filled once by the caller; the merge runs inside the same
+ *          launch: every workgroup of a (b, h) stores its partial, waits for
+ *          the stores to complete and increments the counter, and the
+ *          workgroup that completes the count (splits increments) merges all
+ *          `splits` partials, writes the output and re-arms the counter to 0,
+ *          so the same ticket serves every later call.  Calls that share a
+ *          ticket or the partials must not overlap in time.
  *   out    (B, KVH, G, D) fp16, strides o_sb, o_sh, o_sg.
  *   scale  the score scale, D**-0.5 in the reference.
  */

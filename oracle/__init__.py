@@ -20,6 +20,11 @@ make the restatement trustworthy live in ``tests/test_oracle_*.py``:
 * ``apply_rope_fp16``: torch-CPU half arithmetic and numpy float16
   arithmetic (two independent correctly-rounded implementations), position-0
   identity, fp64 norm preservation, and the whiteboard split-half KAT.
+* ``rope_cos_sin``: fp64 closed form at positions up to 131071 (rotate-half
+  layout, theta, the fp32 angle), and through the whiteboard KAT and the
+  model pin below, which both build their RoPE from it.
+* ``model.prefill`` / ``model.decode_step``: ``transformers.Qwen2ForCausalLM``
+  on a tiny random config, live and through committed logits.
 * ``append_*`` / ``capacity`` / ``decode_slots``: brute-force loops.
 * ``pages_to_dense`` / ``dense_to_pages`` / ``paged_location``: the identity
   block table reduces to a reshape of the dense cache (closed form), and the

@@ -3,11 +3,18 @@ Qwen2-shaped model, fp32-accumulated (test infrastructure only).
 
 ``prefill`` follows ``StudentEngine._prefill`` (SE:679-737) and
 ``decode_step`` follows ``_decode_step_static`` (SE:876-982, math attention
-branch SE:968-972), with every op evaluated in fp32 on fp16 weights.  Pinned
-through its building blocks (``eager_attention``, ``grouped_decode_attention``,
-RoPE, append), each pinned in ``tests/test_oracle.py``, and by the
-prefill/decode consistency test there (the decode step over a prefilled cache
-reproduces the prefill logits of the longer prompt).
+branch SE:968-972), with every op evaluated in fp32 on fp16 weights.  RoPE
+goes through ``rope.rope_cos_sin`` / ``rope.apply_rope_fp32`` (the functions
+the GPU tests feed the kernels), so the pins below cover them too.
+
+Pins (``tests/test_oracle_model.py``): the whole forward -- embedding, fused
+QKV split, RoPE, GQA causal attention, o_proj, RMSNorm, SwiGLU MLP, tied
+lm_head -- against ``transformers.Qwen2ForCausalLM`` (an independent
+implementation of the official model) on a tiny random config, live and
+through the committed logits in ``tests/golden/qwen2_tiny_logits.json``;
+plus the prefill/decode consistency test in ``tests/test_oracle.py`` (the
+decode step over a prefilled cache reproduces the prefill logits of the
+longer prompt).
 """
 
 from __future__ import annotations
@@ -16,7 +23,7 @@ import torch
 import torch.nn.functional as F
 
 from .attention import eager_attention, grouped_decode_attention
-from .rope import rotate_half
+from .rope import apply_rope_fp32, inv_freq, rope_cos_sin
 
 
 def _rms(x, w, eps):
@@ -24,11 +31,10 @@ def _rms(x, w, eps):
     return x * torch.rsqrt(x.pow(2).mean(dim=-1, keepdim=True) + eps) * w
 
 
-def _rope(x, pos, inv_freq):
-    # SE:542-554 in fp32: f = pos * inv_freq, emb = cat(f, f).
-    f = pos.to(torch.float32).unsqueeze(-1) * inv_freq
-    emb = torch.cat((f, f), dim=-1).unsqueeze(1)  # broadcast over heads
-    return x * emb.cos() + rotate_half(x) * emb.sin()
+def _rope(x, pos, inverse_frequency):
+    # SE:542-554 in fp32: the (B, T, D) table of rope_cos_sin, broadcast over heads.
+    cos, sin = rope_cos_sin(pos, inverse_frequency, dtype=torch.float32)
+    return apply_rope_fp32(x, cos.unsqueeze(1), sin.unsqueeze(1))
 
 
 def _f(t):
@@ -51,8 +57,7 @@ def _mlp(x, layer):
 
 
 def inv_freq32(cfg):
-    return 1.0 / (cfg.rope_theta ** (torch.arange(0, cfg.head_dim, 2, dtype=torch.float32)
-                                     / cfg.head_dim))
+    return inv_freq(cfg.head_dim, cfg.rope_theta)
 
 
 def prefill(weights, cfg, input_ids, capacity):

@@ -17,7 +17,7 @@ import torch
 import torch.nn.functional as F
 
 from .attention import eager_attention
-from .rope import apply_rope_fp32
+from .rope import apply_rope_fp32, inv_freq, rope_cos_sin
 
 
 def _rotate_interleaved(x: torch.Tensor) -> torch.Tensor:
@@ -27,14 +27,14 @@ def _rotate_interleaved(x: torch.Tensor) -> torch.Tensor:
 
 def _rope(x: torch.Tensor, theta: float, mode: str) -> torch.Tensor:
     d = x.shape[-1]
-    inv = 1.0 / (theta ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
-    pos = torch.arange(x.shape[-2], dtype=torch.float32)
-    f = torch.outer(pos, inv)
+    inv = inv_freq(d, theta)
+    pos = torch.arange(x.shape[-2])
     if mode == "split_half":
-        emb = torch.cat((f, f), dim=-1)
-        return apply_rope_fp32(x, emb.cos(), emb.sin())
+        # The table and rotation the GPU tests use, so the KAT pins them.
+        cos, sin = rope_cos_sin(pos, inv, dtype=torch.float32)
+        return apply_rope_fp32(x, cos, sin)
     if mode == "interleaved":
-        emb = f.repeat_interleave(2, dim=-1)
+        emb = torch.outer(pos.to(torch.float32), inv).repeat_interleave(2, dim=-1)
         return x * emb.cos() + _rotate_interleaved(x) * emb.sin()
     raise ValueError(f"rope mode {mode!r}")
 

@@ -23,12 +23,14 @@
 //   kPartial  it writes one partial (acc, m, l) in the reference's scratch
 //             layout and a second kernel merges them (the reference's
 //             two-launch shape);
-//   kFused    it writes the partial with write-through (sc1) stores and takes
-//             a device-scope ticket; the last workgroup of the (b, h) merges
-//             all S partials (one wave per query), writes the output and
-//             re-arms the ticket.  Write-through stores plus a wait for their
-//             completion replace an agent-scope release fence, which on this
-//             part writes back the whole L2 per workgroup.
+//   kFused    it writes the partial with write-through (sc1) stores, waits
+//             for them to complete (s_waitcnt vmcnt(0) in every wave, then a
+//             barrier) and takes the (b, h) ticket; the last workgroup of the
+//             (b, h) merges all S partials (one wave per query) with sc1
+//             loads, writes the output and re-arms the ticket.  Every
+//             partial store is an agent-scope atomic store, so the completion
+//             wait is all an agent-scope release has to add here; the full
+//             release fence would also write back the whole L2 per workgroup.
 // Every merge is one pass of independent loads (eight partials per lane in
 // flight) followed by register / permlane / LDS reductions, so it costs one
 // dependent memory round trip.
@@ -474,14 +476,19 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
   }
 
   if (kMode == kFused) {
-    // Wait until this workgroup's write-through stores have completed, then
-    // take the (b, h) ticket; the workgroup that completes the count merges
-    // all S partials -- wave w takes queries w, w + NW, ...; within a wave
-    // lane (sub = lane / 16, d4 = lane % 16) folds partials j = sub (mod 4)
-    // and the four subs merge through permlane swaps -- then re-arms the
-    // ticket.  The ticket of (b, h) is the first of its ceil(S/16) + 1 slots.
-    int32_t* tk = a.ticket + (int64_t)bh * ((S + 15) / 16 + 1);
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    // Publication.  The partial stores above are write-through (sc1) stores,
+    // i.e. relaxed agent-scope atomic stores.  Each wave waits until its own
+    // have been acknowledged (vmcnt counts stores on gfx9); after the barrier
+    // every store of the workgroup has completed, so they precede the ticket
+    // increment in memory order.  The workgroup that completes the count
+    // (one int32 counter per (b, h)) issues its partial loads only after the
+    // increment has returned, and loads with sc1 (relaxed agent-scope atomic
+    // loads), so it reads the stored values.  It merges all S partials --
+    // wave w takes queries w, w + NW, ...; within a wave lane
+    // (sub = lane / 16, d4 = lane % 16) folds partials j = sub (mod 4) and the
+    // four subs merge through permlane swaps -- then re-arms the ticket.
+    int32_t* tk = a.ticket + bh;
+    s_waitcnt_vm(0);
     __syncthreads();
     if (tid == 0) sh_last = (atomicAdd(tk, 1) == S - 1);
     __syncthreads();

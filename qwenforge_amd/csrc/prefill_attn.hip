@@ -396,12 +396,6 @@ __device__ __forceinline__ int swz(int row) {
   return r1 | (r3 << 1) | ((r1 ^ r4) << 2);
 }
 
-__device__ __forceinline__ void s_waitcnt_vm(int n) {
-  // gfx9 encoding: vmcnt[3:0] | expcnt=7 | lgkmcnt=15 | vmcnt[5:4] << 14.
-  if (n == 0) __builtin_amdgcn_s_waitcnt(0x0F70);
-  else __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4)
-}
-
 typedef __attribute__((address_space(3))) void lds_void;
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 

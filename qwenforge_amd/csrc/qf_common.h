@@ -55,6 +55,15 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
                                            0x00020000);
 }
 
+// s_waitcnt vmcnt(n) for n in {0, 4}, leaving the other counters alone.
+// gfx9 encoding: vmcnt[3:0] | expcnt=7 | lgkmcnt=15 | vmcnt[5:4] << 14.
+// On gfx9 vmcnt also counts stores, so vmcnt(0) returns only once every
+// earlier vector store of the wave has been acknowledged.
+__device__ __forceinline__ void s_waitcnt_vm(int n) {
+  if (n == 0) __builtin_amdgcn_s_waitcnt(0x0F70);
+  else __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4)
+}
+
 // fp16(x) for an fp32 value, round-to-nearest-even.
 __device__ __forceinline__ float round16(float x) { return (float)(f16)x; }
 

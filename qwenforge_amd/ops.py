@@ -130,8 +130,13 @@ def make_flash_scratch(batch: int, kv_heads: int, groups: int, capacity: int,
 
 
 def ticket_size(batch: int, kv_heads: int, splits: int) -> int:
-    """int32 counters the single-launch merge needs: one per 16-split group plus one, per (b, h)."""
-    return batch * kv_heads * ((splits + 15) // 16 + 1)
+    """int32 counters the single-launch merge needs: one per (b, kv head).
+
+    ``splits`` does not change the count (the workgroup that completes a
+    (b, h) counter merges all of its partials); it stays in the signature so
+    callers size the ticket from the same arguments as the partials."""
+    del splits
+    return batch * kv_heads
 
 
 def _decode_args(grouped, key_cache, value_cache, attn_bias, flash, kv_last):
@@ -171,6 +176,9 @@ def _scratch_args(grouped, cap, attn_bias, flash, kv_last):
         need = ticket_size(b, kvh, splits)
         if ticket.dtype != torch.int32 or ticket.numel() < need or not ticket.is_contiguous():
             raise ValueError(f"ticket must be a contiguous int32 tensor with {need} elements")
+        if ticket.device != grouped.device:
+            raise ValueError(f"ticket must be on {grouped.device} (got {ticket.device}): the "
+                             "kernel increments it with device-scope atomics")
     kv_last_sb = 0
     if kv_last is not None:
         if kv_last.dtype != torch.int64 or kv_last.device != grouped.device:
