@@ -44,6 +44,11 @@ extern "C" {
 #define QF_OK 0
 #define QF_ERR_INVALID_ARG (-1)
 #define QF_ERR_UNSUPPORTED (-2)
+#define QF_ERR_SCRATCH_LIMIT (-3)
+
+/* Bytes of split partials (acc, m, l) the no-allocation decode entry point
+ * holds per GPU: B*KVH*splits*G*(D+2)*4 must not exceed this. */
+#define QF_NOALLOC_PARTIAL_BYTES (4 << 20)
 
 /* Human-readable text for a return code of any qf_* entry point. */
 const char* qf_error_string(int code);
@@ -94,6 +99,38 @@ int qf_decode_attn(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sg,
                    void* out, int64_t o_sb, int64_t o_sh, int64_t o_sg,
                    int B, int KVH, int G, int D, int cap, float scale,
                    void* stream);
+
+/*
+ * qf_decode_attn without caller scratch.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under hipGraph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).
+ *
+ * Arguments and results are qf_decode_attn's minus acc/m/l/ticket: the
+ * per-split partials and the merge counters live in a static device array of
+ * the library, one copy per GPU (QF_NOALLOC_PARTIAL_BYTES of partials plus
+ * 256 KiB of counters, held until the process ends).  The merge is the one
+ * qf_decode_attn picks for the same split count with a caller ticket for
+ * 2..32 splits and without one above 32, so the output equals
+ * qf_decode_attn's bit for bit.
+ *
+ *   - Returns QF_ERR_SCRATCH_LIMIT (nothing launched) when
+ *     B*KVH*splits*G*(D+2)*4 > QF_NOALLOC_PARTIAL_BYTES.
+ *   - The first call on a device looks the array up with
+ *     hipGetSymbolAddress and zeroes its counters with a fill kernel on
+ *     `stream`; nothing is allocated, ever.
+ *   - Every call on one GPU shares that GPU's array: calls that overlap in
+ *     time on one GPU (different streams, or concurrent graph replays) race
+ *     and must be serialised by the caller.
+ */
+int qf_decode_attn_noalloc(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sg,
+                           const void* k, int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                           const void* v, int64_t v_sb, int64_t v_sh, int64_t v_sn,
+                           const void* bias, int64_t bias_sb,
+                           const int64_t* kv_last, int64_t kv_last_sb,
+                           int splits,
+                           void* out, int64_t o_sb, int64_t o_sh, int64_t o_sg,
+                           int B, int KVH, int G, int D, int cap, float scale,
+                           void* stream);
 
 /*
  * The two launches of the reference's decode, separately (SE:854-865 and

@@ -29,6 +29,17 @@ SIGNATURES = {
         _i32, _i32, _i32, _i32, _i32,   # B, KVH, G, D, cap
         _f32, _vp,                      # scale, stream
     ],
+    "qf_decode_attn_noalloc": [
+        _vp, _i64, _i64, _i64,          # q, q_sb, q_sh, q_sg
+        _vp, _i64, _i64, _i64,          # k, k_sb, k_sh, k_sn
+        _vp, _i64, _i64, _i64,          # v, v_sb, v_sh, v_sn
+        _vp, _i64,                      # bias, bias_sb
+        _vp, _i64,                      # kv_last, kv_last_sb
+        _i32,                           # splits
+        _vp, _i64, _i64, _i64,          # out, o_sb, o_sh, o_sg
+        _i32, _i32, _i32, _i32, _i32,   # B, KVH, G, D, cap
+        _f32, _vp,                      # scale, stream
+    ],
     "qf_decode_split": [
         _vp, _i64, _i64, _i64,          # q
         _vp, _i64, _i64, _i64,          # k

@@ -8,6 +8,9 @@ extern "C" const char* qf_error_string(int code) {
   if (code == QF_ERR_INVALID_ARG)
     return "invalid argument (null pointer, bad size, misaligned pointer or stride)";
   if (code == QF_ERR_UNSUPPORTED) return "unsupported shape (requires head_dim 64 and 1 <= G <= 16)";
+  if (code == QF_ERR_SCRATCH_LIMIT)
+    return "problem too large for the no-allocation scratch "
+           "(B*KVH*splits*G*(D+2)*4 bytes > QF_NOALLOC_PARTIAL_BYTES)";
   if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
   return "unknown error";
 }

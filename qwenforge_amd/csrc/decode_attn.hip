@@ -34,6 +34,8 @@
 // Every merge is one pass of independent loads (eight partials per lane in
 // flight) followed by register / permlane / LDS reductions, so it costs one
 // dependent memory round trip.
+#include <mutex>
+
 #include "qf_common.h"
 #include "../../include/qf_attn.h"
 #include "../../include/qf_paged.h"
@@ -758,5 +760,93 @@ extern "C" int qf_decode_split_paged(const void* q, int64_t q_sb, int64_t q_sh, 
     rc = make_paged(a, kp_sp, vp_sp, block_table, bt_sb, pages_per_row, n_pages, page_size);
   if (rc != QF_OK) return rc;
   launch_split_mode(a, kPartial, static_cast<hipStream_t>(stream));
+  return (int)hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// No-allocation decode: the partials and merge counters of qf_decode_attn in
+// a static device array (one copy per GPU), for callers that cannot allocate.
+// ---------------------------------------------------------------------------
+
+namespace {
+
+constexpr int kNoAllocCounters = 65536;  // one per (b, h); make_args caps B*KVH at 65535
+constexpr int64_t kNoAllocCounterBytes = (int64_t)kNoAllocCounters * 4;
+constexpr int64_t kNoAllocBytes = kNoAllocCounterBytes + QF_NOALLOC_PARTIAL_BYTES;
+constexpr int kMaxDevices = 64;
+
+// Counters first (256 KiB), then acc / m / l of one call.  In host code
+// `scratch` names a host-side stand-in: only the address from
+// hipGetSymbolAddress (noalloc_base) may reach a kernel.
+static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
+std::mutex g_noalloc_mu;
+unsigned char* g_noalloc_base[kMaxDevices] = {};
+
+__global__ __launch_bounds__(256) void zero_counters_kernel(int32_t* p, int n) {
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = 0;
+}
+
+// Device address of this GPU's `scratch` (the current device's).  The first
+// call on a device looks it up and zeroes the counters on `st` with a fill
+// kernel (legal under stream capture, where a memset node is not wanted).
+int noalloc_base(hipStream_t st, unsigned char** base) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return QF_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  if (g_noalloc_base[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (p == nullptr) return (int)hipErrorInvalidSymbol;
+    hipLaunchKernelGGL(zero_counters_kernel, dim3(64), dim3(256), 0, st,
+                       reinterpret_cast<int32_t*>(p), kNoAllocCounters);
+    e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+    g_noalloc_base[dev] = static_cast<unsigned char*>(p);
+  }
+  *base = g_noalloc_base[dev];
+  return QF_OK;
+}
+
+}  // namespace
+
+extern "C" int qf_decode_attn_noalloc(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sg,
+                                      const void* k, int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                                      const void* v, int64_t v_sb, int64_t v_sh, int64_t v_sn,
+                                      const void* bias, int64_t bias_sb,
+                                      const int64_t* kv_last, int64_t kv_last_sb,
+                                      int splits,
+                                      void* out, int64_t o_sb, int64_t o_sh, int64_t o_sg,
+                                      int B, int KVH, int G, int D, int cap, float scale,
+                                      void* stream) {
+  // Shape checks before any HIP call (make_args repeats them on the real pointers).
+  if (D != kD || G < 1 || G > kMaxG) return QF_ERR_UNSUPPORTED;
+  if (B < 1 || KVH < 1 || splits < 1 || splits > 65535 || B * (int64_t)KVH > 65535)
+    return QF_ERR_INVALID_ARG;
+  const int64_t rows = (int64_t)B * KVH * splits * G;
+  const int64_t n_acc = rows * kD;
+  if ((n_acc + 2 * rows) * 4 > (int64_t)QF_NOALLOC_PARTIAL_BYTES) return QF_ERR_SCRATCH_LIMIT;
+  if (!q || !k || !v || !out || cap < 1) return QF_ERR_INVALID_ARG;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  unsigned char* base = nullptr;
+  int rc = noalloc_base(st, &base);
+  if (rc != QF_OK) return rc;
+  float* acc = reinterpret_cast<float*>(base + kNoAllocCounterBytes);
+  float* m = acc + n_acc;
+  float* l = m + rows;
+  // The merge qf_decode_attn uses for this split count with a caller ticket
+  // (single launch) up to 32 splits, and without one (split + combine) above.
+  const int mode = splits == 1 ? kDirect : (splits <= 32 ? kFused : kPartial);
+  int32_t* ticket = mode == kFused ? reinterpret_cast<int32_t*>(base) : nullptr;
+  DecodeArgs a;
+  rc = make_args(a, q, q_sb, q_sh, q_sg, k, k_sb, k_sh, k_sn, v, v_sb, v_sh, v_sn, bias, bias_sb,
+                 kv_last, kv_last_sb, acc, m, l, splits, ticket, out, o_sb, o_sh, o_sg, B, KVH,
+                 G, D, cap, scale, true, true);
+  if (rc != QF_OK) return rc;
+  launch_split_mode(a, mode, st);
+  if (mode == kPartial) launch_combine(a, st);
   return (int)hipGetLastError();
 }

@@ -67,6 +67,24 @@ def test_decode_rejects_bad_arguments_without_launching():
     assert _decode_call(lib, q=18) == -1  # misaligned pointer
 
 
+def test_noalloc_decode_rejects_before_any_hip_call():
+    """Shape, size and pointer checks of qf_decode_attn_noalloc return before the
+    library touches the device (no GPU here)."""
+    lib = _lib.load()
+
+    def call(splits=8, B=1, KVH=2, G=7, D=64, cap=64, q=16):
+        return lib.qf_decode_attn_noalloc(q, 0, 0, 0, 16, 0, 0, 0, 16, 0, 0, 0, None, 0, None, 0,
+                                          splits, 16, 0, 0, 0, B, KVH, G, D, cap, 0.125, None)
+
+    assert call(D=128) == -2
+    assert call(G=17) == -2
+    assert call(splits=0) == -1
+    # 64 x 2 x 64 x 7 partial rows of 66 floats = 15 MB > QF_NOALLOC_PARTIAL_BYTES (4 MiB).
+    assert call(B=64, splits=64) == -3
+    assert call(q=None) == -1
+    assert b"no-allocation scratch" in lib.qf_error_string(-3)
+
+
 def test_prefill_and_append_reject_bad_arguments():
     lib = _lib.load()
     rc = lib.qf_prefill_attn(16, 0, 0, 0, 16, 0, 0, 0, 16, 0, 0, 0, None, None, 0, 0,
