@@ -41,11 +41,17 @@ def _args():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--no-extras", action="store_true", help="headline line only")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--cpu-seconds", type=float, default=16.0,
+                   help="time budget of the attention rows of the CPU baseline (all threads; "
+                        "the one-thread rows take a third more)")
     p.add_argument("--prefill-only", action="store_true",
                    help="time only the config-4 prefill leg (for kernel profiles)")
     p.add_argument("--pmc-sample", action="store_true",
                    help="run a short fixed kernel sequence for rocprofv3 --pmc and exit")
+    p.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                   help="summarise two rocprofv3 --pmc passes over --pmc-sample (FETCH_SIZE, "
+                        "then WRITE_SIZE counter_collection.csv) into "
+                        "profiles/decode_split_cfg2_traffic.json and exit (no GPU)")
     return p.parse_args()
 
 
@@ -136,6 +142,44 @@ def bench_ragged_decode(steps, warmup, dev):
     return dict(ms_per_step=ms, step_bytes=step_bytes, launches=len(layers), splits=splits,
                 replicas=replicas, layers=layers, fused=fused, ms_split=ms_split,
                 ms_combine=ms_combine)
+
+
+def bench_decode_cfg1(steps, warmup, dev):
+    """Config 1: B=1, L=cap=512, one layer (265,728 algorithmic bytes per call).
+    Caches rotated past the MALL (2 x 256 MB of distinct 256 KB caches, 64
+    calls per graph) and, separately, one cache-resident layer called 64 times
+    per graph."""
+    import torch
+
+    from qwenforge_amd import ops, workloads
+
+    base = workloads.decode_uniform(1, 512, seed=0)
+    per = base.key_cache.numel() * 2 * 2
+    reps = -(-2 * MALL_BYTES // per)
+    q = base.grouped.to(dev)
+    k0, v0 = base.key_cache.to(dev), base.value_cache.to(dev)
+    ks = [k0] + [k0.clone() for _ in range(reps - 1)]
+    vs = [v0] + [v0.clone() for _ in range(reps - 1)]
+    splits = ops.choose_splits(1, 2, 512)
+    flash = ops.make_flash_scratch(1, 2, 7, 512, dev, splits=splits)
+    per_graph = 64
+
+    def run_fn(g):
+        def run():
+            for j in range(per_graph):
+                r = (g * per_graph + j) % reps
+                ops.flash_decode_attention(q, ks[r], vs[r], None, flash)
+        return run
+
+    graphs = [GraphStep(run_fn(g)) for g in range(reps // per_graph)]
+    n = max(len(graphs), steps // 4)
+    ms = _time_graphs(graphs, n, max(1, warmup // 4)) / per_graph
+    resident = GraphStep(lambda: [ops.flash_decode_attention(q, k0, v0, None, flash)
+                                  for _ in range(per_graph)])
+    ms_res = _time_graphs([resident], max(8, steps // 4), max(1, warmup // 4)) / per_graph
+    name = ops.decode_kernel_name(1, 2, 7, 512, splits, len(flash) > 4, bias="none")
+    return dict(us_per_layer=ms * 1e3, us_resident=ms_res * 1e3, bytes=base.valid_bytes,
+                splits=splits, kernel=name, caches=reps)
 
 
 def bench_long_decode(steps, warmup, dev):
@@ -407,14 +451,95 @@ def pmc_sample(dev):
                       "split_bytes_mean": sum(c.valid_bytes for c in layers) / len(layers)}))
 
 
-def _traffic():
+def traffic_summary(fetch_csv, write_csv):
+    """HBM bytes per launch of the headline kernel from two PMC passes over
+    ``--pmc-sample``: the 64 MiB device copies calibrate each counter (bytes
+    known to be read / written per copy), then the mean per-dispatch value of
+    the decode kernel is scaled by that factor.  Writes the JSON the bench
+    line's ``roofline.traffic`` reads, stamped with the kernel source hash and
+    instance so that a later kernel change makes the figure stale (null)."""
+    import csv
+    import subprocess
+
+    from qwenforge_amd import ops, workloads
+
+    layers = workloads.decode_ragged_layers(24, 4, seed=0)
+    cap_max = max(c.key_cache.shape[2] for c in layers)
+    splits = ops.choose_splits(4, 2, cap_max)
+    kernel = ops.decode_kernel_name(4, 2, 7, cap_max, splits, ops.prefer_fused(splits))
+    copy_bytes = 64 << 20
+
+    def read(path, counter):
+        rows = [r for r in csv.DictReader(open(path)) if r["Counter_Name"] == counter]
+        copies = [r for r in rows if r["Kernel_Name"].startswith("__amd_rocclr_copyBuffer")]
+        big = max(int(r["Grid_Size"]) for r in copies)
+        cal = [float(r["Counter_Value"]) for r in copies if int(r["Grid_Size"]) == big]
+        ker = [float(r["Counter_Value"]) for r in rows
+               if r["Kernel_Name"].split("(")[0].replace("void ", "").strip() == kernel]
+        if len(cal) < 1 or len(ker) != len(layers):
+            raise SystemExit(f"{path}: {len(cal)} calibration copies, {len(ker)} dispatches of "
+                             f"{kernel} (expected {len(layers)})")
+        return statistics.mean(cal), statistics.mean(ker)
+
+    f_cal, f_ker = read(fetch_csv, "FETCH_SIZE")
+    w_cal, w_ker = read(write_csv, "WRITE_SIZE")
+    f_fac, w_fac = copy_bytes / 1024 / f_cal, copy_bytes / 1024 / w_cal
+    fetch_b, write_b = f_ker * 1024 * f_fac, w_ker * 1024 * w_fac
+    try:
+        commit = subprocess.run(["git", "rev-parse", "--short=12", "HEAD"], cwd=ROOT,
+                                capture_output=True, text=True).stdout.strip() or None
+    except OSError:
+        commit = None
+    rec = {
+        "kernel": kernel,
+        "workload": f"config 2 (B=4 ragged, 24 layers, {splits} splits), one launch per layer",
+        "source_sha16": _kernel_source_hash(),
+        "commit": commit,
+        "fetch_kib_per_launch": round(f_ker, 2),
+        "write_kib_per_launch": round(w_ker, 2),
+        "copy_calibration": {"bytes_read": copy_bytes, "bytes_written": copy_bytes,
+                             "FETCH_SIZE_kib": round(f_cal, 2), "WRITE_SIZE_kib": round(w_cal, 2),
+                             "fetch_factor": round(f_fac, 5), "write_factor": round(w_fac, 5)},
+        "algorithmic_bytes_per_launch": int(sum(c.valid_bytes for c in layers) / len(layers)),
+        "fetch_bytes_per_launch": int(fetch_b),
+        "write_bytes_per_launch": int(write_b),
+        "traffic_bytes_per_launch": int(fetch_b + write_b),
+    }
+    path = os.path.join(ROOT, "profiles", "decode_split_cfg2_traffic.json")
+    with open(path, "w") as f:
+        json.dump(rec, f, indent=1)
+        f.write("\n")
+    print(json.dumps(rec))
+
+
+def _kernel_source_hash():
+    """sha256 prefix of the decode kernel's source (decode_attn.hip + qf_common.h)."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for name in ("decode_attn.hip", "qf_common.h"):
+        with open(os.path.join(ROOT, "qwenforge_amd", "csrc", name), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def _traffic(kernel):
     """HBM bytes per launch of the headline's dominant kernel, measured with
-    rocprofv3 counters (profiles/decode_split_cfg2_traffic.json)."""
+    rocprofv3 counters (profiles/decode_split_cfg2_traffic.json), with the
+    source hash and kernel instance the passes ran.  None when the kernel
+    source or instance has changed since (the figure would be stale)."""
     path = os.path.join(ROOT, "profiles", "decode_split_cfg2_traffic.json")
     if not os.path.exists(path):
-        return None
+        return None, "no counter passes recorded"
     with open(path) as f:
-        return json.load(f).get("traffic_bytes_per_launch")
+        rec = json.load(f)
+    if rec.get("source_sha16") != _kernel_source_hash():
+        return None, "stale: the decode kernel source changed after the counter passes"
+    if rec.get("kernel") != kernel:
+        return None, f"stale: the counter passes ran {rec.get('kernel')}"
+    return rec.get("traffic_bytes_per_launch"), (
+        f"rocprofv3 FETCH_SIZE + WRITE_SIZE passes at commit {rec.get('commit', '?')}, "
+        f"source {rec['source_sha16']}")
 
 
 def _cpu_model():
@@ -428,22 +553,26 @@ def _cpu_model():
     return "unknown"
 
 
-def _time_oracle(layers, seconds, threads):
-    """Config-2 layer calls of the CPU oracle for about `seconds` at `threads`
-    threads (3 warm-up calls first); returns (GB/s, calls, median s, total s)."""
+def _time_oracle(layers, seconds, threads, form="fp32"):
+    """Decode-attention layer calls of the CPU oracle for about `seconds` at
+    `threads` threads (3 warm-up calls first, at least 20 timed calls);
+    `form` is "fp32" (the fp32-accumulated oracle) or "fp16" (the reference's
+    own fp16 form, SE:968-971).  Returns (GB/s, calls, median s, total s)."""
     import torch
 
     import oracle
 
+    fn = (oracle.grouped_decode_attention if form == "fp32"
+          else oracle.grouped_decode_attention_fp16)
     torch.set_num_threads(threads)
     for c in layers[:3]:
-        oracle.grouped_decode_attention(c.grouped, c.key_cache, c.value_cache, c.bias)
+        fn(c.grouped, c.key_cache, c.value_cache, c.bias)
     t_end = time.perf_counter() + seconds
     done_bytes, n_layers, times = 0, 0, []
     while time.perf_counter() < t_end or n_layers < 20:
         c = layers[n_layers % len(layers)]
         t0 = time.perf_counter()
-        oracle.grouped_decode_attention(c.grouped, c.key_cache, c.value_cache, c.bias)
+        fn(c.grouped, c.key_cache, c.value_cache, c.bias)
         times.append(time.perf_counter() - t0)
         done_bytes += c.valid_bytes
         n_layers += 1
@@ -451,28 +580,91 @@ def _time_oracle(layers, seconds, threads):
     return done_bytes / total / 1e9, n_layers, statistics.median(times), total
 
 
-def cpu_baseline(layers, seconds):
-    """The CPU oracle (fp32 restatement of SE:939-972) on config-2 layers,
-    timed on the host's cores (all affine threads; then one thread on a
-    third of the time budget)."""
-    threads = len(os.sched_getaffinity(0))
-    gbs, n, med, total = _time_oracle(layers, seconds, threads)
-    gbs1, n1, med1, total1 = _time_oracle(layers, seconds / 3, 1)
+def _cpu_row(layers, seconds, threads, form, what):
+    gbs, n, med, total = _time_oracle(layers, seconds, threads, form)
+    gbs1, n1, med1, total1 = _time_oracle(layers, seconds / 3, 1, form)
     return {
-        "value": round(gbs, 3),
+        "GBps": round(gbs, 3), "us_per_layer": round(med * 1e6, 1), "threads": threads,
+        "sample": f"{n} {what} layer calls ({form}), median {med * 1e6:.0f} us/layer, "
+                  f"{total:.1f} s total",
+        "single_thread": {"GBps": round(gbs1, 3), "us_per_layer": round(med1 * 1e6, 1),
+                          "sample": f"{n1} calls, {total1:.1f} s"},
+    }
+
+
+def _cpu_decode_step(threads, reps=4):
+    """Config 5 on the CPU: the fp32 oracle's decode step (SE:876-982,
+    oracle.model.decode_step) of the full Qwen2.5-0.5B shape at B=1 and B=4
+    over 1152-slot caches with 1024 valid slots.  The cache holds random
+    values (the step's work does not depend on them), so no CPU prefill runs;
+    weights are upcast to fp32 once, outside the timed region."""
+    import torch
+
+    import oracle.model as om
+    from qwenforge_amd.model import Qwen2Config, init_weights
+
+    torch.set_num_threads(threads)
+    cfg = Qwen2Config()
+    w16 = init_weights(cfg, "cpu", seed=0)
+    embed = w16["embed"].float()
+    w = {"embed": embed, "final_norm": w16["final_norm"].float(), "lm_head": embed,
+         "layers": [{k: v.float() for k, v in layer.items()} for layer in w16["layers"]]}
+    del w16
+    out = {}
+    gen = torch.Generator().manual_seed(0)
+    for b in (1, 4):
+        caches = [(torch.randn(b, 2, 1152, 64, generator=gen),
+                   torch.randn(b, 2, 1152, 64, generator=gen)) for _ in range(cfg.layers)]
+        tok = torch.randint(0, cfg.vocab, (b,), generator=gen)
+        times = []
+        for i in range(reps + 1):
+            t0 = time.perf_counter()
+            om.decode_step(w, cfg, tok, torch.full((b,), 1024 + i), caches, 1024 + i)
+            times.append(time.perf_counter() - t0)
+        med = statistics.median(times[1:])
+        out[f"tok_s_bs{b}"] = round(b / med, 2)
+        out[f"ms_per_step_bs{b}"] = round(med * 1e3, 1)
+    out["sample"] = (f"{reps} timed steps per batch after one warm-up, fp32 oracle decode step, "
+                     "24 layers + lm_head, 1024 valid cache slots")
+    return out
+
+
+def cpu_baseline(layers, seconds):
+    """The CPU restatements timed on the host's cores, per BASELINE's CPU plan:
+    the fp32 oracle (SE:939-972 / SE:629-661 restated) and the reference's own
+    fp16 form (SE:968-971), on config-2 layers (the headline `value`: fp32,
+    all affine threads) and on config 1, each at all threads and at one; plus
+    the config-5 decode step in fp32."""
+    from qwenforge_amd import workloads
+
+    threads = len(os.sched_getaffinity(0))
+    share = seconds / 4
+    cfg1 = [workloads.decode_uniform(1, 512, seed=i) for i in range(8)]
+    c2_32 = _cpu_row(layers, share * 1.6, threads, "fp32", "config-2")
+    c2_16 = _cpu_row(layers, share * 0.8, threads, "fp16", "config-2")
+    c1_32 = _cpu_row(cfg1, share * 0.8, threads, "fp32", "config-1")
+    c1_16 = _cpu_row(cfg1, share * 0.8, threads, "fp16", "config-1")
+    return {
+        "value": c2_32["GBps"],
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{n} config-2 layer calls (B=4 ragged, fp32 oracle), "
-                  f"median {med * 1e6:.0f} us/layer, {total:.1f} s total",
-        "single_thread": {"value": round(gbs1, 3), "unit": "GB/s",
-                          "sample": f"{n1} calls, median {med1 * 1e6:.0f} us/layer, {total1:.1f} s"},
+        "sample": "config 2 (B=4 ragged) layer calls of the fp32 oracle: " + c2_32["sample"],
+        "single_thread": {"value": c2_32["single_thread"]["GBps"], "unit": "GB/s",
+                          "sample": c2_32["single_thread"]["sample"]},
+        "config2": {"fp32_oracle": c2_32, "fp16_reference_form": c2_16},
+        "config1": {"fp32_oracle": c1_32, "fp16_reference_form": c1_16,
+                    "what": "B=1, L=512, 14q/2kv, hd64, one layer (265,728 B)"},
+        "config5": _cpu_decode_step(threads),
         "cpu_model": _cpu_model(),
     }
 
 
 def main():
     args = _args()
+    if args.traffic_from:
+        traffic_summary(*args.traffic_from)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
               "(every box here has one MI355X)", file=sys.stderr)
@@ -496,6 +688,11 @@ def main():
         return
 
     r = bench_ragged_decode(args.steps, args.warmup, dev)
+    from qwenforge_amd import ops
+
+    cap_max = max(c.key_cache.shape[2] for c in r["layers"])
+    kernel = ops.decode_kernel_name(4, 2, 7, cap_max, r["splits"], r["fused"])
+    traffic, traffic_src = _traffic(kernel)
     ms = r["ms_per_step"]
     gbs = r["step_bytes"] / (ms * 1e-3) / 1e9
     us_layer = ms * 1e3 / r["launches"]
@@ -531,11 +728,11 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(split_gbs / HBM_PEAK_GBS, 4),
-            "traffic": _traffic(),
-            "kernel": ("qf::decode_split_kernel<8, 1, 2, false> (qf_decode_attn: 8 waves, vector bias, "
-                       "single-launch merge, dense cache; the whole call)" if r["fused"] else
-                       "qf::decode_split_kernel<8, 1, 1, false> (qf_decode_split: 8 waves, vector bias, "
-                       "partial mode, dense cache)"),
+            "traffic": traffic,
+            "traffic_source": traffic_src,
+            "kernel": kernel,
+            "kernel_role": ("qf_decode_attn: the whole call is this one launch (single-launch merge)"
+                            if r["fused"] else "qf_decode_split: the split launch (partial mode)"),
             "bytes_per_launch": int(launch_bytes),
             "avg_launch_us": round(us_split, 3),
             "combine_kernel_avg_us": (None if r["ms_combine"] is None
@@ -544,6 +741,18 @@ def main():
         },
     }
     if not args.no_extras:
+        c1 = bench_decode_cfg1(args.steps, args.warmup, dev)
+        line["decode_cfg1"] = {
+            "us_per_layer": round(c1["us_per_layer"], 3),
+            "GBps": round(c1["bytes"] / (c1["us_per_layer"] * 1e-6) / 1e9, 1),
+            "hbm_frac": round(c1["bytes"] / (c1["us_per_layer"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "us_per_layer_cache_resident": round(c1["us_resident"], 3),
+            "bytes_per_layer": c1["bytes"],
+            "splits": c1["splits"],
+            "kernel": c1["kernel"],
+            "what": f"B=1, L=cap=512, no bias; {c1['caches']} distinct caches rotated past the "
+                    "MALL, 64 graph-replayed calls per graph",
+        }
         lg = bench_long_decode(args.steps, args.warmup, dev)
         line["long_decode_cfg3"] = {
             "us_per_layer": round(lg["us_per_layer"], 3),

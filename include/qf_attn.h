@@ -30,7 +30,8 @@
  *     Nothing throws across the ABI.
  *   - Supported shapes: head_dim D == 64, 1 <= G <= 16 query heads per kv
  *     head.  Anything else returns QF_ERR_UNSUPPORTED.
- *   - Reentrant; no global mutable state.
+ *   - Reentrant.  The only global state is the per-GPU address of
+ *     qf_decode_attn_noalloc's static scratch, looked up once under a mutex.
  */
 #ifndef QF_ATTN_H
 #define QF_ATTN_H
@@ -99,6 +100,15 @@ int qf_decode_attn(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sg,
                    void* out, int64_t o_sb, int64_t o_sh, int64_t o_sg,
                    int B, int KVH, int G, int D, int cap, float scale,
                    void* stream);
+
+/*
+ * Launch plan of the decode split kernel (host only, no GPU work): the
+ * wave64 count per workgroup qf_decode_attn / qf_decode_split launch with
+ * for these arguments (`fused` = a ticket is passed), or QF_ERR_INVALID_ARG.
+ * The kernel is decode_split_kernel<waves, bias, merge mode, paged>; tools
+ * use this to name the kernel a measurement covers.
+ */
+int qf_decode_waves(int B, int KVH, int G, int cap, int splits, int fused);
 
 /*
  * qf_decode_attn without caller scratch.  No counterpart in the reference:

@@ -14,6 +14,9 @@ make the restatement trustworthy live in ``tests/test_oracle_*.py``:
   library routine), against fp64 brute-force loops, and against the
   reference's whiteboard known-answer logits (causal attention + split-half
   RoPE).
+* ``grouped_decode_attention_fp16`` (the reference's fp16 form, timed as a
+  CPU baseline only): within fp16 rounding of fp64 SDPA, exact on uniform V
+  and on a single valid key, fp16 output.
 * ``split_partials`` / ``combine_partials``: invariants (independence of the
   split count, S=1 equals the unsplit path, empty and fully masked splits,
   single valid key, uniform V, key permutation).
@@ -40,6 +43,7 @@ from .attention import (  # noqa: F401
     eager_attention,
     flash_decode,
     grouped_decode_attention,
+    grouped_decode_attention_fp16,
     split_partials,
 )
 from .rope import (  # noqa: F401

@@ -77,6 +77,27 @@ def grouped_decode_attention(
     return torch.matmul(probs, v)
 
 
+def grouped_decode_attention_fp16(
+    grouped: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    attn_bias: torch.Tensor | None = None,
+    scale: float | None = None,
+) -> torch.Tensor:
+    """The reference's own fp16 form of the graph-step math attention
+    (SE:968-971), for the CPU baseline: ``scores = (grouped @ K^T) * scale``
+    and ``+ bias`` in fp16, ``softmax(scores.float())`` rounded to fp16, then
+    ``probabilities @ V`` in fp16.  Returns fp16 (B, KVH, G, D).
+    """
+    d = grouped.shape[-1]
+    scale = d ** -0.5 if scale is None else scale
+    scores = torch.matmul(grouped, key_cache.transpose(-2, -1)) * scale
+    if attn_bias is not None:
+        scores = scores + attn_bias[:, None, None, :]
+    probabilities = torch.softmax(scores.float(), dim=-1).to(grouped.dtype)
+    return torch.matmul(probabilities, value_cache)
+
+
 def split_partials(
     grouped: torch.Tensor,
     key_cache: torch.Tensor,

@@ -29,6 +29,7 @@ SIGNATURES = {
         _i32, _i32, _i32, _i32, _i32,   # B, KVH, G, D, cap
         _f32, _vp,                      # scale, stream
     ],
+    "qf_decode_waves": [_i32, _i32, _i32, _i32, _i32, _i32],   # B, KVH, G, cap, splits, fused
     "qf_decode_attn_noalloc": [
         _vp, _i64, _i64, _i64,          # q, q_sb, q_sh, q_sg
         _vp, _i64, _i64, _i64,          # k, k_sb, k_sh, k_sn

@@ -669,6 +669,18 @@ extern "C" int qf_decode_attn(const void* q, int64_t q_sb, int64_t q_sh, int64_t
   return (int)hipGetLastError();
 }
 
+extern "C" int qf_decode_waves(int B, int KVH, int G, int cap, int splits, int fused) {
+  if (G < 1 || G > kMaxG || B < 1 || KVH < 1 || cap < 1 || splits < 1 || splits > 65535)
+    return QF_ERR_INVALID_ARG;
+  DecodeArgs a{};
+  a.B = B;
+  a.KVH = KVH;
+  a.G = G;
+  a.cap = cap;
+  a.splits = splits;
+  return pick_waves(a, splits == 1 ? kDirect : (fused ? kFused : kPartial));
+}
+
 extern "C" int qf_decode_split(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sg,
                                const void* k, int64_t k_sb, int64_t k_sh, int64_t k_sn,
                                const void* v, int64_t v_sb, int64_t v_sh, int64_t v_sn,

@@ -39,6 +39,15 @@ from .model import Qwen2Config
 from .rope import cos_sin, inv_freq
 
 
+def cache_capacity(prompt_len: int, new_tokens: int, multiple: int = 64) -> int:
+    """KV slots per row for a prompt of ``prompt_len`` tokens and ``new_tokens``
+    greedy tokens on the graph path (SE:1263-1273): the prompt plus the
+    ``new_tokens - 1`` decode steps that append (the last token is never fed
+    back), at least the prompt, rounded up to ``multiple``."""
+    cap = max(prompt_len + max(new_tokens - 1, 0), prompt_len)
+    return (cap + multiple - 1) // multiple * multiple
+
+
 class DecodeEngine:
     """Batched greedy decoding of a Qwen2-shaped model on one MI355X."""
 
@@ -326,7 +335,7 @@ class DecodeEngine:
         b = len(prompts)
         lengths = [int(p.numel()) for p in prompts]
         p_max = max(lengths)
-        cap = (p_max + max(max_new_tokens - 1, 0) + 63) // 64 * 64
+        cap = cache_capacity(p_max, max_new_tokens)
         caches = self.new_caches(b, cap)
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
         ev[0].record()
@@ -364,7 +373,7 @@ class DecodeEngine:
         (HIP events on the current stream).
         """
         b, s = input_ids.shape
-        cap = (s + max(max_new_tokens - 1, 0) + 63) // 64 * 64
+        cap = cache_capacity(s, max_new_tokens)
         caches = self.new_caches(b, cap)
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
         ev[0].record()

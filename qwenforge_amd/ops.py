@@ -139,6 +139,19 @@ def ticket_size(batch: int, kv_heads: int, splits: int) -> int:
     return batch * kv_heads
 
 
+def decode_kernel_name(batch: int, kv_heads: int, groups: int, capacity: int, splits: int,
+                       fused: bool, bias: str = "vec", paged: bool = False) -> str:
+    """Name of the split-kernel instance a decode call launches, from the
+    library's own launch plan (``qf_decode_waves``): decode_split_kernel<waves,
+    bias (0 none, 1 16-byte vector, 2 scalar), mode (0 direct, 1 partial, 2
+    single-launch merge), paged>."""
+    waves = _lib.load().qf_decode_waves(batch, kv_heads, groups, capacity, splits, int(fused))
+    _lib.check(min(waves, 0), "qf_decode_waves")
+    mode = 0 if splits == 1 else (2 if fused else 1)
+    kind = {"none": 0, "vec": 1, "scalar": 2}[bias]
+    return f"qf::decode_split_kernel<{waves}, {kind}, {mode}, {str(paged).lower()}>"
+
+
 def _decode_args(grouped, key_cache, value_cache, attn_bias, flash, kv_last):
     """Validate the decode operands; returns the parsed pieces."""
     _require_cuda_fp16("grouped", grouped, 4)

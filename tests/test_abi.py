@@ -67,6 +67,16 @@ def test_decode_rejects_bad_arguments_without_launching():
     assert _decode_call(lib, q=18) == -1  # misaligned pointer
 
 
+def test_decode_launch_plan_names_the_kernel():
+    from qwenforge_amd import ops
+
+    # Config 2 (B=4, cap 2048, 16 splits, single-launch merge, vector bias).
+    assert ops.decode_kernel_name(4, 2, 7, 2048, 16, True) == "qf::decode_split_kernel<8, 1, 2, false>"
+    # One workgroup per kv head streams everything with 16 waves.
+    assert _lib.load().qf_decode_waves(1, 2, 7, 512, 1, 0) == 16
+    assert _lib.load().qf_decode_waves(1, 2, 0, 512, 1, 0) == -1
+
+
 def test_noalloc_decode_rejects_before_any_hip_call():
     """Shape, size and pointer checks of qf_decode_attn_noalloc return before the
     library touches the device (no GPU here)."""

@@ -8,6 +8,7 @@ greedy token is fed to both sides -- so near-ties cannot cascade.
 import pytest
 import torch
 
+import oracle
 import oracle.model as om
 from qwenforge_amd.engine import DecodeEngine
 from qwenforge_amd.model import Qwen2Config, init_weights, weights_to
@@ -17,19 +18,37 @@ pytestmark = pytest.mark.gpu
 LOGIT_TOL = 3e-2
 
 
+def _fp32(w):
+    """fp32 copy of a weight dict (the oracle's upcasts then copy nothing)."""
+    embed = w["embed"].float()
+    return {"embed": embed, "final_norm": w["final_norm"].float(), "lm_head": embed,
+            "layers": [{k: v.float() for k, v in layer.items()} for layer in w["layers"]]}
+
+
 @pytest.mark.parametrize("batch", [1, 4])
 def test_teacher_forced_logits_match_oracle(dev, batch):
-    cfg = Qwen2Config(layers=2)
+    _teacher_forced(dev, Qwen2Config(layers=2), batch, 200, 6, (200 + 6 + 63) // 64 * 64)
+
+
+@pytest.mark.parametrize("batch", [1, 4])
+def test_full_shape_teacher_forced_logits_match_oracle(dev, batch):
+    """Config 5 at its real shape: 24 layers, vocab 151936, a 1024-token
+    prefix in a cache of oracle.capacity(1024, 128) = 1152 slots (SE:1263-1273),
+    8 teacher-forced graph replays of the captured step (SE:876-982)."""
+    _teacher_forced(dev, Qwen2Config(), batch, 1024, 8, oracle.capacity(1024, 128))
+
+
+def _teacher_forced(dev, cfg, batch, s, steps, cap):
     w_cpu = init_weights(cfg, "cpu", seed=0)
+    w_ref = _fp32(w_cpu)
     eng = DecodeEngine(cfg, weights_to(w_cpu, dev), dev)
     gen = torch.Generator().manual_seed(batch)
-    s, steps = 200, 6
     ids = torch.randint(0, cfg.vocab, (batch, s), generator=gen)
-    cap = (s + steps + 63) // 64 * 64
     caches = eng.new_caches(batch, cap)
     logits = eng.prefill(ids.to(dev), caches).float().cpu()
-    ref_logits, ref_caches = om.prefill(w_cpu, cfg, ids, cap)
-    print(f"[engine B={batch}] prefill max|dlogit| {(logits - ref_logits).abs().max():.3e}", flush=True)
+    ref_logits, ref_caches = om.prefill(w_ref, cfg, ids, cap)
+    print(f"[engine L={cfg.layers} B={batch} S={s}] prefill max|dlogit| "
+          f"{(logits - ref_logits).abs().max():.3e}", flush=True)
     assert (logits - ref_logits).abs().max().item() <= LOGIT_TOL
     for (kc, vc), (rk, rv) in zip(caches, ref_caches):
         assert (kc.float().cpu() - rk).abs().max().item() <= 2e-2
@@ -45,9 +64,9 @@ def test_teacher_forced_logits_match_oracle(dev, batch):
         ctx["graph"].replay()
         torch.cuda.synchronize()
         got = ctx["logits"].float().cpu()
-        ref = om.decode_step(w_cpu, cfg, teacher, torch.full((batch,), s + t), ref_caches, s + t)
+        ref = om.decode_step(w_ref, cfg, teacher, torch.full((batch,), s + t), ref_caches, s + t)
         err = (got - ref).abs().max().item()
-        print(f"[engine B={batch}] step {t} max|dlogit| {err:.3e}", flush=True)
+        print(f"[engine L={cfg.layers} B={batch}] step {t} max|dlogit| {err:.3e}", flush=True)
         assert err <= LOGIT_TOL, f"step {t}"
         top2 = ref.topk(2, dim=-1).values
         clear = (top2[:, 0] - top2[:, 1]) > 2 * LOGIT_TOL
@@ -92,15 +111,42 @@ def test_graph_replay_equals_eager_step_full_shape(dev):
     assert bool(torch.isfinite(graph_logits.float()).all())
 
 
-def test_generate_full_shape_runs(dev):
+@pytest.mark.parametrize("batch", [1, 4])
+def test_generate_full_shape_128_tokens(dev, batch):
+    """The bench's config-5 run: 1024-token prefix, 128 greedy tokens.  The
+    cache capacity is the reference's rule (SE:1263-1273) and after 127
+    replays the device-side bookkeeping (SE:1126-1132) stands at write slot
+    1024 + 127 = 1151, positions 1151 and step 128."""
     cfg = Qwen2Config()
     eng = DecodeEngine(cfg, init_weights(cfg, dev, seed=2), dev)
-    ids = torch.randint(0, cfg.vocab, (4, 1024), generator=torch.Generator().manual_seed(1)).to(dev)
+    ids = torch.randint(0, cfg.vocab, (batch, 1024),
+                        generator=torch.Generator().manual_seed(1)).to(dev)
     timing = {}
-    rows = eng.generate(ids, 16, timing)
-    assert rows.shape == (4, 16)
+    rows = eng.generate(ids, 128, timing)
+    ctx = eng._ctx
+    assert rows.shape == (batch, 128)
     assert int(rows.min()) >= 0 and int(rows.max()) < cfg.vocab
     assert timing["decode_ms"] > 0
+    assert ctx["caches"][0][0].shape[2] == oracle.capacity(1024, 128) == 1152
+    assert int(ctx["write"].item()) == 1151 and int(ctx["step"].item()) == 128
+    assert ctx["pos"].cpu().tolist() == [1151] * batch
+    assert torch.equal(rows[:, 1:], ctx["rows"][:, 1:])
+
+
+def test_generate_ragged_full_shape_bookkeeping(dev):
+    """Ragged prompts at full shape: capacity from the longest prompt, shared
+    write slot p_max + 127 and per-row positions len_b + 127 after 127 replays."""
+    cfg = Qwen2Config()
+    eng = DecodeEngine(cfg, init_weights(cfg, dev, seed=2), dev)
+    gen = torch.Generator().manual_seed(7)
+    lengths = (512, 700, 896, 1024)
+    prompts = [torch.randint(0, cfg.vocab, (n,), generator=gen).to(dev) for n in lengths]
+    rows = eng.generate_ragged(prompts, 128)
+    ctx = eng._ctx
+    assert rows.shape == (4, 128)
+    assert ctx["caches"][0][0].shape[2] == oracle.capacity(1024, 128)
+    assert int(ctx["write"].item()) == 1024 + 127
+    assert ctx["pos"].cpu().tolist() == [n + 127 for n in lengths]
 
 
 def test_fused_step_matches_torch_step(dev):

@@ -42,3 +42,15 @@ def test_workgroups_fill_cus_once_or_twice(batch):
             (batch, length, s)
         # Splits keep at least one 32-key tile.
         assert -(-length // s) >= 32
+
+
+def test_engine_capacity_rule_equals_oracle():
+    """The engine's KV capacity (engine.cache_capacity, used by generate and
+    generate_ragged) against the oracle's restatement of SE:1263-1273."""
+    import oracle
+    from qwenforge_amd.engine import cache_capacity
+
+    for p in list(range(1, 200, 3)) + [511, 512, 1023, 1024, 1025, 2048]:
+        for n in (0, 1, 2, 3, 63, 64, 65, 127, 128, 129, 300):
+            assert cache_capacity(p, n) == oracle.capacity(p, n), (p, n)
+    assert cache_capacity(1024, 128) == 1152

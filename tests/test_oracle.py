@@ -101,6 +101,34 @@ def test_grouped_decode_equals_repeat_path_and_brute_force():
             assert np.abs(np.array(rows) - got[bb, h].numpy()).max() < 1e-9
 
 
+def test_grouped_decode_fp16_form_within_fp16_rounding_of_sdpa():
+    """The reference's fp16 math form (SE:968-971): fp16 scores, fp32 softmax
+    rounded to fp16, fp16 PV.  Against fp64 SDPA it is off by fp16 rounding
+    only; uniform V and a single unmasked key are reproduced exactly."""
+    gen = torch.Generator().manual_seed(31)
+    b, kvh, g, cap = 2, 2, 7, 300
+    q = _rand(gen, b, kvh, g, 64)
+    k = _rand(gen, b, kvh, cap, 64)
+    v = _rand(gen, b, kvh, cap, 64)
+    bias = torch.zeros(b, cap, dtype=torch.float16)
+    bias[1, 200:] = oracle.FP16_MIN
+    got = oracle.grouped_decode_attention_fp16(q, k, v, bias)
+    assert got.dtype == torch.float16
+    mask = (bias == 0)[:, None, None, :].expand(b, kvh, g, cap)
+    ref = F.scaled_dot_product_attention(q.double(), k.double(), v.double(), attn_mask=mask)
+    err = (got.double() - ref).abs().max().item()
+    assert err < 4e-3, err
+    assert err > 0  # it really rounds (an fp32 path would sit near 1e-6)
+    row = _rand(gen, 64)
+    uni = row.expand(b, kvh, cap, 64).contiguous()
+    assert torch.equal(oracle.grouped_decode_attention_fp16(q, k, uni, bias),
+                       row.expand(b, kvh, g, 64))
+    one = torch.full((b, cap), oracle.FP16_MIN, dtype=torch.float16)
+    one[:, 17] = 0
+    assert torch.equal(oracle.grouped_decode_attention_fp16(q, k, v, one),
+                       v[:, :, 17:18].expand(b, kvh, g, 64))
+
+
 def test_grouped_decode_head_mapping_is_h_div_g():
     """Query head h of the flattened (B, 14) layout must read kv head h // 7."""
     gen = torch.Generator().manual_seed(3)
