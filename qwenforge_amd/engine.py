@@ -143,12 +143,13 @@ class DecodeEngine:
         (slots [0, len_b) of row b) and the causal attention of every row.
         """
         return self._prefill_packed(
-            prompts, lambda i, q, k, v, cu, n, cos, sin: ops.prefill_varlen(
-                q, k, v, cu, n, cos, sin, caches[i][0], caches[i][1], 0))
+            prompts, lambda i, q, k, v, cu, n, cos, sin, lengths: ops.prefill_varlen(
+                q, k, v, cu, n, cos, sin, caches[i][0], caches[i][1], 0, lengths=lengths))
 
     def _prefill_packed(self, prompts, attend):
         """Packed ragged prefill body; ``attend(layer, q, k, v, cu, max_len, cos,
-        sin)`` runs the varlen RoPE + append + attention launch of one layer."""
+        sin, lengths)`` runs the varlen RoPE + append + attention launch of one
+        layer (``lengths``: the host row lengths ``cu`` was built from)."""
         cfg = self.cfg
         dev = self.device
         lengths = [int(p.numel()) for p in prompts]
@@ -169,7 +170,7 @@ class DecodeEngine:
             q = proj[:, :qw].view(total, cfg.heads, cfg.head_dim)
             k = proj[:, qw:qw + kvw].view(total, cfg.kv_heads, cfg.head_dim)
             v = proj[:, qw + kvw:].view(total, cfg.kv_heads, cfg.head_dim)
-            att = attend(i, q, k, v, cu, max(lengths), cos, sin)
+            att = attend(i, q, k, v, cu, max(lengths), cos, sin, lengths)
             hidden = residual + F.linear(att.reshape(total, cfg.hidden), layer["o_weight"])
             residual = hidden
             hidden = residual + self._mlp(self._rms(hidden, layer["post_norm"]), layer)

@@ -413,10 +413,43 @@ def _prefill_launch(query, key, value, out, cos=None, sin=None, key_cache=None,
     return out
 
 
+def check_cu_seqlens(cu_seqlens: torch.Tensor, total: int, max_seqlen: int,
+                     lengths=None) -> None:
+    """Host check of packed-row offsets before a ragged prefill launch.
+
+    The kernels clamp each row to ``max_seqlen`` and to ``[0, total)`` so that
+    nothing reads or writes out of bounds, but tokens past a row's clamp
+    would be neither attended nor appended.  So: ``cu[0] == 0``, non-
+    decreasing, ``cu[B] == total`` and no row longer than ``max_seqlen``.
+    ``lengths`` (host ints, the rows' token counts) lets a caller that built
+    ``cu_seqlens`` from them skip the device read; otherwise the offsets are
+    copied to the host (a synchronisation), except under graph capture, where
+    they cannot be read and the caller owns the precondition.
+    """
+    if lengths is not None:
+        cu = [0]
+        for n in lengths:
+            cu.append(cu[-1] + int(n))
+    elif cu_seqlens.is_cuda and torch.cuda.is_current_stream_capturing():
+        return
+    else:
+        cu = [int(x) for x in cu_seqlens.tolist()]
+    if len(cu) != cu_seqlens.numel():
+        raise ValueError(f"cu_seqlens has {cu_seqlens.numel()} entries, lengths describe {len(cu)}")
+    if cu[0] != 0 or cu[-1] != total:
+        raise ValueError(f"cu_seqlens must start at 0 and end at T={total} (got {cu[0]}, {cu[-1]})")
+    rows = [b - a for a, b in zip(cu, cu[1:])]
+    if min(rows) < 0:
+        raise ValueError("cu_seqlens must be non-decreasing")
+    if max(rows) > max_seqlen:
+        raise ValueError(f"a row holds {max(rows)} tokens > max_seqlen={max_seqlen}")
+
+
 def prefill_varlen(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                    cu_seqlens: torch.Tensor, max_seqlen: int, cos: torch.Tensor | None = None,
                    sin: torch.Tensor | None = None, key_cache: torch.Tensor | None = None,
-                   value_cache: torch.Tensor | None = None, start_pos: int = 0) -> torch.Tensor:
+                   value_cache: torch.Tensor | None = None, start_pos: int = 0,
+                   lengths=None) -> torch.Tensor:
     """Ragged causal prefill of packed rows (``_prefill_ragged``, SE:1162-1204, in one launch).
 
     query (T, QH, 64), key/value (T, KVH, 64): rows packed along the token axis;
@@ -424,7 +457,9 @@ def prefill_varlen(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
     [cu[b], cu[b+1]).  Optional ``cos``/``sin`` (T, 64) per-token tables (each
     row's own positions) rotate q and k; with ``key_cache``/``value_cache``
     (B, KVH, cap, 64) token i of row b is written to slot start_pos + i of row
-    b (RoPE needs the caches).  Returns (T, QH, 64).
+    b (RoPE needs the caches).  ``lengths`` (optional host ints) are the rows'
+    token counts ``cu_seqlens`` was built from (see ``check_cu_seqlens``).
+    Returns (T, QH, 64).
     """
     for n, t in (("query", query), ("key", key), ("value", value)):
         _require_cuda_fp16(n, t, 3)
@@ -437,6 +472,7 @@ def prefill_varlen(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
     b = cu_seqlens.numel() - 1
     if b < 1 or not 1 <= max_seqlen <= t_:
         raise ValueError(f"need B >= 1 rows and 1 <= max_seqlen <= T (got {b}, {max_seqlen})")
+    check_cu_seqlens(cu_seqlens, t_, max_seqlen, lengths)
     cs_sn = 0
     if (cos is None) != (sin is None):
         raise ValueError("cos and sin go together")

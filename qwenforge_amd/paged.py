@@ -24,7 +24,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
-from .ops import HEAD_DIM, _ptr, _require_cuda_fp16, _scratch_args, _stream
+from .ops import HEAD_DIM, _ptr, _require_cuda_fp16, _scratch_args, _stream, check_cu_seqlens
 from .step_ops import PACK_ROPE, _batch, _check, _rows, _weight, rope_args
 
 MIN_PAGE, MAX_PAGE = 64, 4096
@@ -246,7 +246,8 @@ def rope_append_paged(query: torch.Tensor, key: torch.Tensor, value: torch.Tenso
 def prefill_varlen_paged(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                          cu_seqlens: torch.Tensor, max_seqlen: int, cos: torch.Tensor | None,
                          sin: torch.Tensor | None, k_pool: torch.Tensor, v_pool: torch.Tensor,
-                         block_table: torch.Tensor, start_pos: int = 0) -> torch.Tensor:
+                         block_table: torch.Tensor, start_pos: int = 0,
+                         lengths=None) -> torch.Tensor:
     """``ops.prefill_varlen`` appending into paged caches.
 
     Packed query (T, QH, 64), key/value (T, KVH, 64); cu_seqlens (B+1,) int32
@@ -265,6 +266,7 @@ def prefill_varlen_paged(query: torch.Tensor, key: torch.Tensor, value: torch.Te
     b = cu_seqlens.numel() - 1
     if b < 1 or not 1 <= max_seqlen <= t_:
         raise ValueError(f"need B >= 1 rows and 1 <= max_seqlen <= T (got {b}, {max_seqlen})")
+    check_cu_seqlens(cu_seqlens, t_, max_seqlen, lengths)
     if start_pos % 64:
         raise ValueError("start_pos must be a multiple of 64")
     pool, cap = _pool_args(k_pool, v_pool, block_table, b)

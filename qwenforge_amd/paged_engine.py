@@ -58,8 +58,9 @@ class PagedDecodeEngine(DecodeEngine):
         else:
             table = kv.table[torch.tensor(rows, device=self.device)]
         return self._prefill_packed(
-            prompts, lambda i, q, k, v, cu, n, cos, sin: paged.prefill_varlen_paged(
-                q, k, v, cu, n, cos, sin, kv.pools[i][0], kv.pools[i][1], table, 0))
+            prompts, lambda i, q, k, v, cu, n, cos, sin, lengths: paged.prefill_varlen_paged(
+                q, k, v, cu, n, cos, sin, kv.pools[i][0], kv.pools[i][1], table, 0,
+                lengths=lengths))
 
     # ------------------------------------------------------------------ decode
     def make_paged_context(self, kv: paged.PagedKvCache, batch: int, n_cols: int):

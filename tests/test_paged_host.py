@@ -47,3 +47,25 @@ def test_page_size_rules(page):
     with pytest.raises(ValueError):
         paged.PagedKvCache(layers=1, kv_heads=2, n_pages=4, page_size=page, max_rows=1,
                            pages_per_row=1, device="cpu")
+
+
+def test_check_cu_seqlens_rejects_bad_offsets():
+    """Host validation of ragged-prefill offsets (CPU tensors suffice: the
+    check reads them on the host)."""
+    import torch
+
+    from qwenforge_amd.ops import check_cu_seqlens
+
+    cu = torch.tensor([0, 3, 7, 12], dtype=torch.int32)
+    check_cu_seqlens(cu, 12, 5)
+    check_cu_seqlens(cu, 12, 5, lengths=[3, 4, 5])
+    bad = [
+        (torch.tensor([0, 3, 7, 11], dtype=torch.int32), 12, 5, None),   # does not end at T
+        (torch.tensor([1, 3, 7, 12], dtype=torch.int32), 12, 5, None),   # does not start at 0
+        (torch.tensor([0, 8, 7, 12], dtype=torch.int32), 12, 8, None),   # decreasing
+        (cu, 12, 4, None),                                              # a row longer than max_seqlen
+        (cu, 12, 5, [3, 4]),                                            # lengths of the wrong row count
+    ]
+    for c, total, mx, lengths in bad:
+        with pytest.raises(ValueError):
+            check_cu_seqlens(c, total, mx, lengths)
