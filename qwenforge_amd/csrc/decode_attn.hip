@@ -49,6 +49,12 @@ constexpr int kMaxG = 16;
 
 enum Mode { kDirect = 0, kPartial = 1, kFused = 2 };
 
+// Merge mode of a call with `splits` partials; `ticket`: the caller passed
+// merge counters (single launch).
+constexpr int merge_mode(int splits, bool ticket) {
+  return splits == 1 ? kDirect : (ticket ? kFused : kPartial);
+}
+
 struct DecodeArgs {
   const f16* q;
   int64_t q_sb, q_sh, q_sg;
@@ -158,37 +164,101 @@ __device__ __forceinline__ void fold_partials(const DecodeArgs& a, int bh, int q
   const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a.acc + pbase * G * kD, (int64_t)S * G * kD * 4);
   const __amdgpu_buffer_rsrc_t rm = buffer_rsrc(a.m + pbase * G, (int64_t)S * G * 4);
   const __amdgpu_buffer_rsrc_t rl = buffer_rsrc(a.l + pbase * G, (int64_t)S * G * 4);
-  for (; j0 < S; j0 += 8 * step) {
-    float mv[8], lv[8];
-    f32x4 av[8];
+  // Partial u of a batch sits a uniform distance past partial 0: the lane's
+  // offsets are computed once per batch and u's distance goes in the
+  // scalar offset, so a batch costs registers for its data only.
+  constexpr int kBatch = 8;
+  const int ml_step = step * G * 4, acc_step = step * G * kD * 4;
+  for (; j0 < S; j0 += kBatch * step) {
+    const int row0 = j0 * G + q;
+    const int ml_off = row0 * 4, acc_off = (row0 * kD + 4 * d4) * 4;
+    float mv[kBatch], lv[kBatch];
+    f32x4 av[kBatch];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int j = j0 + step * u;
-      const int row = j * G + q;
-      mv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rm, row * 4, 0, aux));
-      lv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, row * 4, 0, aux));
+    for (int u = 0; u < kBatch; ++u) {
       av[u] = __builtin_bit_cast(
-          f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, (row * kD + 4 * d4) * 4, 0, aux));
+          f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, acc_off, u * acc_step, aux));
+      mv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rm, ml_off, u * ml_step, aux));
+      lv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, ml_off, u * ml_step, aux));
     }
+    // Keep every load of the batch above this point: left alone, the
+    // scheduler sinks loads next to their uses to save registers, and the
+    // batch becomes a chain of dependent round trips.
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < kBatch; ++u)
       if (j0 + step * u >= S) mv[u] = kNegInf;
     float mc = mv[0];
 #pragma unroll
-    for (int u = 1; u < 8; ++u) mc = fmaxf(mc, mv[u]);
+    for (int u = 1; u < kBatch; ++u) mc = fmaxf(mc, mv[u]);
     const float mn = fmaxf(M, mc);
     const float safe = (mn == kNegInf) ? 0.f : mn;
     const float r = (M == kNegInf) ? 0.f : fast_exp2((M - safe) * kLog2e);
     L *= r;
     A *= r;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < kBatch; ++u) {
       const float wu = (mv[u] == kNegInf) ? 0.f : fast_exp2((mv[u] - safe) * kLog2e);
       L += wu * lv[u];
       A += wu * av[u];
     }
     M = mn;
   }
+}
+
+// Single-launch merge of query q of (b, h) = bh by one wave: lane
+// (sub = lane / 16, d4 = lane % 16) folds partials j = sub + 4u (u < kB,
+// j < S <= 4 kB) of dims 4*d4 .. +3 into (M, L, A).  Each partial's (m, l)
+// is loaded once per wave -- lane j loads partial j's -- and handed to the
+// folding lanes with ds_bpermute, so a wave issues 2 + kB vector memory
+// instructions (the m/l loads of the 16 lanes that share a partial would
+// otherwise be 16 identical requests each), all before the first wait: one
+// round trip.  sc1 loads: the partials come from other workgroups' sc1
+// stores.
+template <int kB>
+__device__ __forceinline__ void merge_query(const DecodeArgs& a, int bh, int q, int lane, float& M,
+                                            float& L, f32x4& A) {
+  const int G = a.G, S = a.splits;
+  const int sub = lane >> 4, d4 = lane & 15;
+  const int64_t pbase = (int64_t)bh * S;
+  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a.acc + pbase * G * kD, (int64_t)S * G * kD * 4);
+  const __amdgpu_buffer_rsrc_t rm = buffer_rsrc(a.m + pbase * G, (int64_t)S * G * 4);
+  const __amdgpu_buffer_rsrc_t rl = buffer_rsrc(a.l + pbase * G, (int64_t)S * G * 4);
+  // Lanes >= S read past the partials: the buffer returns 0 (masked below).
+  const float m_mine = __builtin_bit_cast(
+      float, __builtin_amdgcn_raw_buffer_load_b32(rm, (lane * G + q) * 4, 0, kSc1));
+  const float l_mine = __builtin_bit_cast(
+      float, __builtin_amdgcn_raw_buffer_load_b32(rl, (lane * G + q) * 4, 0, kSc1));
+  const int acc_off = ((sub * G + q) * kD + 4 * d4) * 4, acc_step = 4 * G * kD * 4;
+  f32x4 av[kB];
+#pragma unroll
+  for (int u = 0; u < kB; ++u)
+    av[u] = __builtin_bit_cast(
+        f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, acc_off, u * acc_step, kSc1));
+  __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before the first wait
+  float mv[kB], lv[kB];
+#pragma unroll
+  for (int u = 0; u < kB; ++u) {
+    const int j = sub + 4 * u;
+    mv[u] = __shfl(m_mine, j);
+    lv[u] = __shfl(l_mine, j);
+    if (j >= S) mv[u] = kNegInf;
+  }
+  float mn = mv[0];
+#pragma unroll
+  for (int u = 1; u < kB; ++u) mn = fmaxf(mn, mv[u]);
+  const float safe = (mn == kNegInf) ? 0.f : mn;
+  float Ls = 0.f;
+  f32x4 As = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < kB; ++u) {
+    const float wu = (mv[u] == kNegInf) ? 0.f : fast_exp2((mv[u] - safe) * kLog2e);
+    Ls += wu * lv[u];
+    As += wu * av[u];
+  }
+  M = mn;
+  L = Ls;
+  A = As;
 }
 
 // fp16 out[b, h, q, 4*d4 .. +3] = A / L.
@@ -487,8 +557,9 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     // increment has returned, and loads with sc1 (relaxed agent-scope atomic
     // loads), so it reads the stored values.  It merges all S partials --
     // wave w takes queries w, w + NW, ...; within a wave lane
-    // (sub = lane / 16, d4 = lane % 16) folds partials j = sub (mod 4) and the
-    // four subs merge through permlane swaps -- then re-arms the ticket.
+    // (sub = lane / 16, d4 = lane % 16) folds partials j = sub (mod 4)
+    // (merge_query) and the four subs merge through permlane swaps -- then
+    // re-arms the ticket.
     int32_t* tk = a.ticket + bh;
     s_waitcnt_vm(0);
     __syncthreads();
@@ -498,7 +569,9 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     for (int q = w; q < G; q += NW) {
       float Mq = kNegInf, Lq = 0.f;
       f32x4 Aq = {0.f, 0.f, 0.f, 0.f};
-      fold_partials<true>(a, bh, q, lane & 15, lane >> 4, 4, Mq, Lq, Aq);
+      if (S <= 16) merge_query<4>(a, bh, q, lane, Mq, Lq, Aq);
+      else if (S <= 32) merge_query<8>(a, bh, q, lane, Mq, Lq, Aq);
+      else fold_partials<true>(a, bh, q, lane & 15, lane >> 4, 4, Mq, Lq, Aq);
       lse_merge_lanes<false>(Mq, Lq, Aq);
       lse_merge_lanes<true>(Mq, Lq, Aq);
       if (lane < 16) store_out(a, bh, q, lane, Lq, Aq);
@@ -663,7 +736,7 @@ extern "C" int qf_decode_attn(const void* q, int64_t q_sb, int64_t q_sh, int64_t
                            o_sb, o_sh, o_sg, B, KVH, G, D, cap, scale, true, true);
   if (rc != QF_OK) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int mode = splits == 1 ? kDirect : (ticket != nullptr ? kFused : kPartial);
+  const int mode = merge_mode(splits, ticket != nullptr);
   launch_split_mode(a, mode, st);
   if (mode == kPartial) launch_combine(a, st);
   return (int)hipGetLastError();
@@ -678,7 +751,7 @@ extern "C" int qf_decode_waves(int B, int KVH, int G, int cap, int splits, int f
   a.G = G;
   a.cap = cap;
   a.splits = splits;
-  return pick_waves(a, splits == 1 ? kDirect : (fused ? kFused : kPartial));
+  return pick_waves(a, merge_mode(splits, fused != 0));
 }
 
 extern "C" int qf_decode_split(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sg,
@@ -748,7 +821,7 @@ extern "C" int qf_decode_attn_paged(const void* q, int64_t q_sb, int64_t q_sh, i
     rc = make_paged(a, kp_sp, vp_sp, block_table, bt_sb, pages_per_row, n_pages, page_size);
   if (rc != QF_OK) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int mode = splits == 1 ? kDirect : (ticket != nullptr ? kFused : kPartial);
+  const int mode = merge_mode(splits, ticket != nullptr);
   launch_split_mode(a, mode, st);
   if (mode == kPartial) launch_combine(a, st);
   return (int)hipGetLastError();
@@ -851,7 +924,7 @@ extern "C" int qf_decode_attn_noalloc(const void* q, int64_t q_sb, int64_t q_sh,
   float* l = m + rows;
   // The merge qf_decode_attn uses for this split count with a caller ticket
   // (single launch) up to 32 splits, and without one (split + combine) above.
-  const int mode = splits == 1 ? kDirect : (splits <= 32 ? kFused : kPartial);
+  const int mode = merge_mode(splits, splits <= 32);
   int32_t* ticket = mode == kFused ? reinterpret_cast<int32_t*>(base) : nullptr;
   DecodeArgs a;
   rc = make_args(a, q, q_sb, q_sh, q_sg, k, k_sb, k_sh, k_sn, v, v_sb, v_sh, v_sn, bias, bias_sb,
