@@ -102,8 +102,8 @@ def bench_ragged_decode(steps, warmup, dev):
     set_bytes = sum(c.key_cache.numel() * 2 * 2 for c in layers)
     replicas = max(2, -(-2 * MALL_BYTES // set_bytes))
     cap_max = max(c.key_cache.shape[2] for c in layers)
-    splits = ops.choose_splits(4, 2, cap_max)
-    flash = ops.make_flash_scratch(4, 2, 7, cap_max, dev, splits=splits)
+    splits, fused = ops.decode_plan(4, 2, cap_max)
+    flash = ops.make_flash_scratch(4, 2, 7, cap_max, dev, splits=splits, fused=fused)
     sets = []
     for _ in range(replicas):
         sets.append([c.to(dev) for c in layers])
@@ -160,8 +160,8 @@ def bench_decode_cfg1(steps, warmup, dev):
     k0, v0 = base.key_cache.to(dev), base.value_cache.to(dev)
     ks = [k0] + [k0.clone() for _ in range(reps - 1)]
     vs = [v0] + [v0.clone() for _ in range(reps - 1)]
-    splits = ops.choose_splits(1, 2, 512)
-    flash = ops.make_flash_scratch(1, 2, 7, 512, dev, splits=splits)
+    splits, fused = ops.decode_plan(1, 2, 512)
+    flash = ops.make_flash_scratch(1, 2, 7, 512, dev, splits=splits, fused=fused)
     per_graph = 64
 
     def run_fn(g):
@@ -194,8 +194,8 @@ def bench_long_decode(steps, warmup, dev):
     q = base.grouped.to(dev)
     ks = [base.key_cache.to(dev) for _ in range(reps)]
     vs = [base.value_cache.to(dev) for _ in range(reps)]
-    splits = ops.choose_splits(1, 2, 32768)
-    flash = ops.make_flash_scratch(1, 2, 7, 32768, dev, splits=splits)
+    splits, fused = ops.decode_plan(1, 2, 32768)
+    flash = ops.make_flash_scratch(1, 2, 7, 32768, dev, splits=splits, fused=fused)
     per_graph = 8
 
     def run_fn(g):
@@ -226,8 +226,8 @@ def bench_bandwidth_decode(steps, warmup, dev, batch, length):
     k0, v0 = base.key_cache.to(dev), base.value_cache.to(dev)
     ks = [k0] + [k0.clone() for _ in range(reps - 1)]
     vs = [v0] + [v0.clone() for _ in range(reps - 1)]
-    splits = ops.choose_splits(batch, 2, length)
-    flash = ops.make_flash_scratch(batch, 2, 7, length, dev, splits=splits)
+    splits, fused = ops.decode_plan(batch, 2, length)
+    flash = ops.make_flash_scratch(batch, 2, 7, length, dev, splits=splits, fused=fused)
 
     def full():
         for r in range(reps):
@@ -276,8 +276,8 @@ def bench_paged_decode(steps, warmup, dev, batch, length, page=64):
     for r in range(1, reps):
         kp[r], vp[r] = kp[0].clone(), vp[0].clone()
     del k0, v0
-    splits = ops.choose_splits(batch, 2, length)
-    flash = ops.make_flash_scratch(batch, 2, 7, length, dev, splits=splits)
+    splits, fused = ops.decode_plan(batch, 2, length)
+    flash = ops.make_flash_scratch(batch, 2, 7, length, dev, splits=splits, fused=fused)
 
     def full():
         for r in range(reps):
@@ -440,7 +440,8 @@ def pmc_sample(dev):
     torch.cuda.synchronize()
     layers = [c.to(dev) for c in workloads.decode_ragged_layers(24, 4, seed=0)]
     cap_max = max(c.key_cache.shape[2] for c in layers)
-    flash = ops.make_flash_scratch(4, 2, 7, cap_max, dev, splits=ops.choose_splits(4, 2, cap_max))
+    splits, fused = ops.decode_plan(4, 2, cap_max)
+    flash = ops.make_flash_scratch(4, 2, 7, cap_max, dev, splits=splits, fused=fused)
     for c in layers:
         kv_last = torch.tensor([n - 1 for n in c.lengths], dtype=torch.int64, device=dev)
         ops.flash_decode_attention(c.grouped, c.key_cache, c.value_cache, c.bias, flash,
@@ -465,8 +466,8 @@ def traffic_summary(fetch_csv, write_csv):
 
     layers = workloads.decode_ragged_layers(24, 4, seed=0)
     cap_max = max(c.key_cache.shape[2] for c in layers)
-    splits = ops.choose_splits(4, 2, cap_max)
-    kernel = ops.decode_kernel_name(4, 2, 7, cap_max, splits, ops.prefer_fused(splits))
+    splits, fused = ops.decode_plan(4, 2, cap_max)
+    kernel = ops.decode_kernel_name(4, 2, 7, cap_max, splits, fused)
     copy_bytes = 64 << 20
 
     def read(path, counter):

@@ -8,6 +8,7 @@ from . import ops  # noqa: F401  (registers the student_qwen:: custom ops)
 from .ops import (  # noqa: F401
     choose_splits,
     decode_attention,
+    decode_plan,
     flash_decode_attention,
     gqa_flash_prefill,
     gqa_flash_prefill_rope_append,

@@ -59,9 +59,47 @@ def _require_cuda_fp16(name: str, t: torch.Tensor, ndim: int | None = None) -> N
 # decode
 # --------------------------------------------------------------------------
 
-def choose_splits(batch: int, kv_heads: int, length: int, min_keys: int = 64,
-                  target_workgroups: int = NUM_CUS) -> int:
-    """Split count for the decode kernel on MI355X.
+def decode_plan(batch: int, kv_heads: int, length: int) -> tuple[int, bool]:
+    """(split count, single-launch merge) for a decode call over rows of
+    ``length`` slots on MI355X (256 CUs).
+
+    Up to 16 (b, kv head) pairs (measured on MI355X over 1-16 pairs and
+    1024-32768 slots, every split count from 1 to 256 in both merge modes):
+
+    * short rows (``length <= 2048``, or ``<= 4096`` with at most 2 pairs):
+      the single-launch merge, splits of about 128 keys (64 with at most 2
+      pairs), at most 32 splits and at most 192 workgroups -- e.g. config 2
+      (B=4, cap 2048): 16 splits; B=8, L=2048: 12;
+    * longer rows: split + combine launches, splits of about 128 keys, at
+      least 256 and at most 1024 workgroups, at most 128 splits -- e.g.
+      config 3 (B=1, L=32768): 128; B=4, L=8192: 64 (10.9 us against
+      12.2 us for 32 splits with the single-launch merge; B=8, L=8192: 13.2
+      against 15.7).
+
+    More pairs keep the fill rule of ``_fill_splits``.  (The reference's
+    rule, ``max(1, min(32, 272 // (B*KVH), cap // 256))`` at SE:1027, targets
+    68 SMs and always uses two launches.)
+    """
+    pairs = max(1, batch * kv_heads)
+    if pairs > 16:
+        s = _fill_splits(pairs, length)
+        return s, prefer_fused(s)
+    if length <= 2048 or (length <= 4096 and pairs <= 2):
+        keys = 64 if pairs <= 2 else 128
+        s = max(1, min(math.ceil(length / keys), 192 // pairs, 32))
+        return s, s > 1
+    s = max(1, min(max(length // 128, NUM_CUS // pairs), 128, 4 * NUM_CUS // pairs))
+    return s, False
+
+
+def choose_splits(batch: int, kv_heads: int, length: int) -> int:
+    """Split count of ``decode_plan``."""
+    return decode_plan(batch, kv_heads, length)[0]
+
+
+def _fill_splits(pairs: int, length: int, min_keys: int = 128,
+                 target_workgroups: int = NUM_CUS) -> int:
+    """Split count for more than 16 (b, kv head) pairs.
 
     The (split, b, kv-head) workgroups fill the CUs once -- floor(CUs / pairs)
     splits -- or twice (two eight-wave workgroups share a CU) when that still
@@ -71,19 +109,10 @@ def choose_splits(batch: int, kv_heads: int, length: int, min_keys: int = 64,
     merge at all).  A count just above one per CU leaves a few CUs with a
     second workgroup and costs up to 30% (measured: B=12 L=5760 at 11 splits,
     264 workgroups, 16.7 us vs 13.1 us at 10).  Splits are never shorter than
-    ``min_keys`` slots (twice that with 8 or more (b, kv head) pairs, where
-    fewer, longer splits shorten the merge).  With at most 8 pairs and splits
-    of >= 1024 keys the count doubles, so each wave keeps at most a few
-    dependent tiles.  Where 32 splits still leave short splits (<= 256 keys),
-    the count stops at 32 so that the single-launch merge applies (its merging
-    workgroup folds all S partials in one pass up to S = 32).  Measured on
-    MI355X from 0.26 MB to 268 MB of K/V (config 2: 16 splits, fused; B=1,
-    L=4096: 32, fused; B=1, L=32768: 128, two launches; B=16, L=32768: 8,
-    fused; B=12, L=5760: 21, fused).  (The reference's rule,
-    ``max(1, min(32, 272 // (B*KVH), cap // 256))`` at SE:1027, targets 68 SMs.)
+    ``min_keys`` slots.  Measured on MI355X (B=12, L=5760: 21 splits, fused;
+    B=16, L=32768: 8, fused; B=64, L=4096: 2, fused).
     """
-    pairs = max(1, batch * kv_heads)
-    by_len = max(1, math.ceil(length / (2 * min_keys if pairs >= 8 else min_keys)))
+    by_len = max(1, math.ceil(length / min_keys))
     s = max(1, target_workgroups // pairs)
     s2 = 2 * target_workgroups // pairs
     twice = 1 < s2 <= 32 and length <= 512 * s2
@@ -91,18 +120,15 @@ def choose_splits(batch: int, kv_heads: int, length: int, min_keys: int = 64,
         twice = s > 1 and length >= 256 * s2
     if twice:
         s = s2
-    if pairs <= 8 and length / s >= 1024:
-        s *= 2
-    if s > 32 and length <= 32 * 256:
-        s = 32
     return max(1, min(by_len, s, 1024))
 
 
 def prefer_fused(splits: int) -> bool:
-    """Single-launch merge (the last workgroup of each (b, kv head) merges)
-    pays off up to 32 splits, where the merging wave folds at most eight
-    partials per lane in one round trip; above that the second (combine)
-    launch is cheaper (measured on MI355X)."""
+    """Merge mode for an explicit split count without a shape: the
+    single-launch merge (the last workgroup of each (b, kv head) merges) up to
+    32 splits, where each of its lanes folds at most eight partials in one
+    round trip; above that the second (combine) launch is cheaper (measured on
+    MI355X).  ``decode_plan`` picks the mode per shape."""
     return 1 < splits <= 32
 
 
@@ -113,10 +139,13 @@ def make_flash_scratch(batch: int, kv_heads: int, groups: int, capacity: int,
 
     Returns ``(acc, m, l, out)`` -- the reference's tuple -- plus a zeroed
     int32 ``ticket`` (``ticket_size`` counters) when ``fused`` (single-launch
-    merge; default ``prefer_fused(splits)``).  All addresses stay fixed, so
-    the tuple can be captured into a hipGraph.
+    merge).  Defaults: ``decode_plan`` for the shape when ``splits`` is None,
+    else ``prefer_fused(splits)``.  All addresses stay fixed, so the tuple can
+    be captured into a hipGraph.
     """
-    splits = choose_splits(batch, kv_heads, capacity) if splits is None else splits
+    if splits is None:
+        splits, planned = decode_plan(batch, kv_heads, capacity)
+        fused = planned if fused is None else fused
     fused = prefer_fused(splits) if fused is None else fused
     f32 = dict(device=device, dtype=torch.float32)
     acc = torch.zeros(batch, kv_heads, splits, groups, head_dim, **f32)

@@ -10,36 +10,53 @@ import pytest
 from qwenforge_amd import ops
 
 
-@pytest.mark.parametrize("batch,length,splits", [
-    (1, 512, 8),       # config 1: splits of >= 64 keys
-    (4, 2048, 16),     # config 2 (cap 2048): >= 128 keys with 8 pairs
-    (1, 32768, 128),   # config 3: two launches
-    (1, 4096, 32),     # the single-launch merge's limit
-    (16, 32768, 8),    # bandwidth regime: one workgroup per CU
-    (64, 4096, 2),
-    (12, 5760, 21),    # the reference's benchmark shape: two per CU, fused
-    (20, 4096, 12),
-    (100, 4096, 1),    # 200 pairs: one split, no merge
-    (8, 4096, 16),     # one per CU fits exactly; twice would give 128-key splits
-    (16, 4096, 16),    # exact fit, but 256-key splits: twice
-    (32, 1024, 4),
-    (128, 1024, 1),    # 256 pairs: one split per row fills the chip, no merge
+@pytest.mark.parametrize("batch,length,splits,fused", [
+    (1, 512, 8, True),       # config 1: 64-key splits, single launch
+    (4, 2048, 16, True),     # config 2 (cap 2048): 128-key splits, single launch
+    (1, 32768, 128, False),  # config 3: split + combine
+    (1, 4096, 32, True),     # <= 2 pairs and <= 4096 keys: single launch
+    (1, 8192, 128, False),   # 8.6 us against 9.3 for 32 fused splits
+    (2, 4096, 64, False),
+    (4, 4096, 32, False),    # 9.5 us against 10.6
+    (4, 8192, 64, False),    # 10.9 us against 12.2
+    (8, 2048, 12, True),     # at most 192 workgroups with the single launch
+    (8, 4096, 32, False),    # 11.0 us against 11.9
+    (8, 16384, 64, False),   # at most 1024 workgroups
+    (16, 32768, 8, True),    # bandwidth regime: one workgroup per CU
+    (64, 4096, 2, True),
+    (12, 5760, 21, True),    # the reference's benchmark shape: two per CU, fused
+    (20, 4096, 12, True),
+    (100, 4096, 1, False),   # 200 pairs: one split, no merge
+    (16, 4096, 16, True),    # exact fit, but 256-key splits: twice
+    (32, 1024, 4, True),
+    (128, 1024, 1, False),   # 256 pairs: one split per row fills the chip, no merge
 ])
-def test_choose_splits_at_benchmark_shapes(batch, length, splits):
+def test_decode_plan_at_benchmark_shapes(batch, length, splits, fused):
+    assert ops.decode_plan(batch, 2, length) == (splits, fused)
     assert ops.choose_splits(batch, 2, length) == splits
 
 
 @pytest.mark.parametrize("batch", list(range(1, 129)))
-def test_workgroups_fill_cus_once_or_twice(batch):
+def test_workgroup_counts_stay_in_the_measured_ranges(batch):
     for length in (512, 1024, 2048, 4096, 5760, 8192, 16384, 32768):
-        s = ops.choose_splits(batch, 2, length)
-        wg = 2 * batch * s
+        s, fused = ops.decode_plan(batch, 2, length)
+        pairs, wg = 2 * batch, 2 * batch * s
+        assert 1 <= s <= 128
+        assert fused == (s > 1 and (pairs > 16 and s <= 32 or pairs <= 16 and fused))
+        if fused:
+            assert s <= 32  # the single-launch merge folds <= 8 partials per lane
         if s == 1:
-            continue  # at least as many pairs as CUs: nothing to split
-        # Either at most one workgroup per CU, or two per CU with the
-        # single-launch merge, or a long-context case with <= 8 pairs.
-        assert wg <= ops.NUM_CUS or (s <= 32 and wg <= 2 * ops.NUM_CUS) or 2 * batch <= 8, \
-            (batch, length, s)
+            continue  # at least as many pairs as CUs, or a row too short to split
+        if pairs <= 16:
+            # Single launch: at most 192 workgroups; two launches: from a full
+            # fill of the CUs (floor(CUs / pairs) splits, never a count just
+            # above it) to four per CU, or 128 splits.
+            full = ops.NUM_CUS // pairs * pairs
+            assert (wg <= 192) if fused else (full <= wg <= 4 * ops.NUM_CUS or s == 128), \
+                (batch, length, s)
+        else:
+            # Once per CU, or twice with the single-launch merge.
+            assert wg <= ops.NUM_CUS or (s <= 32 and wg <= 2 * ops.NUM_CUS), (batch, length, s)
         # Splits keep at least one 32-key tile.
         assert -(-length // s) >= 32
 
