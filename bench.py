@@ -46,6 +46,8 @@ def _args():
                         "the one-thread rows take a third more)")
     p.add_argument("--prefill-only", action="store_true",
                    help="time only the config-4 prefill leg (for kernel profiles)")
+    p.add_argument("--only", choices=("cfg1", "cfg2", "cfg3", "prefill", "e2e"),
+                   help="time one leg and print its JSON (for per-leg kernel profiles)")
     p.add_argument("--pmc-sample", action="store_true",
                    help="run a short fixed kernel sequence for rocprofv3 --pmc and exit")
     p.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -593,7 +595,7 @@ def _cpu_row(layers, seconds, threads, form, what):
     }
 
 
-def _cpu_decode_step(threads, reps=4):
+def _cpu_decode_step(threads, reps=5):
     """Config 5 on the CPU: the fp32 oracle's decode step (SE:876-982,
     oracle.model.decode_step) of the full Qwen2.5-0.5B shape at B=1 and B=4
     over 1152-slot caches with 1024 valid slots.  The cache holds random
@@ -613,20 +615,29 @@ def _cpu_decode_step(threads, reps=4):
     del w16
     out = {}
     gen = torch.Generator().manual_seed(0)
+    state = {}
     for b in (1, 4):
         caches = [(torch.randn(b, 2, 1152, 64, generator=gen),
                    torch.randn(b, 2, 1152, 64, generator=gen)) for _ in range(cfg.layers)]
-        tok = torch.randint(0, cfg.vocab, (b,), generator=gen)
-        times = []
-        for i in range(reps + 1):
+        state[b] = (caches, torch.randint(0, cfg.vocab, (b,), generator=gen))
+    # Warm-up steps at both batch sizes first (thread pool, first touch of the
+    # fp32 weights), then the timed steps, alternating the batch sizes.
+    for b in (1, 4, 1, 4):
+        caches, tok = state[b]
+        om.decode_step(w, cfg, tok, torch.full((b,), 1024), caches, 1024)
+    times = {1: [], 4: []}
+    for i in range(reps):
+        for b in (1, 4):
+            caches, tok = state[b]
             t0 = time.perf_counter()
-            om.decode_step(w, cfg, tok, torch.full((b,), 1024 + i), caches, 1024 + i)
-            times.append(time.perf_counter() - t0)
-        med = statistics.median(times[1:])
+            om.decode_step(w, cfg, tok, torch.full((b,), 1025 + i), caches, 1025 + i)
+            times[b].append(time.perf_counter() - t0)
+    for b in (1, 4):
+        med = statistics.median(times[b])
         out[f"tok_s_bs{b}"] = round(b / med, 2)
         out[f"ms_per_step_bs{b}"] = round(med * 1e3, 1)
-    out["sample"] = (f"{reps} timed steps per batch after one warm-up, fp32 oracle decode step, "
-                     "24 layers + lm_head, 1024 valid cache slots")
+    out["sample"] = (f"median of {reps} timed steps per batch (after two warm-up steps at each), "
+                     "fp32 oracle decode step, 24 layers + lm_head, 1024 valid cache slots")
     return out
 
 
@@ -661,6 +672,25 @@ def cpu_baseline(layers, seconds):
     }
 
 
+def _only(leg, steps, warmup, dev):
+    """One leg's figures, for profiling a leg's kernels by themselves."""
+    if leg == "cfg1":
+        r = bench_decode_cfg1(steps, warmup, dev)
+        return {"decode_cfg1": {k: r[k] for k in ("us_per_layer", "us_resident", "splits", "kernel")}}
+    if leg == "cfg2":
+        r = bench_ragged_decode(steps, warmup, dev)
+        return {"decode_cfg2": {"us_per_layer": r["ms_per_step"] * 1e3 / r["launches"],
+                                "splits": r["splits"], "fused": r["fused"]}}
+    if leg == "cfg3":
+        return {"long_decode_cfg3": bench_long_decode(steps, warmup, dev)}
+    if leg == "prefill":
+        pf = bench_prefill(steps, warmup, dev)
+        return {"prefill_cfg4": {"us_per_layer": pf["us_per_layer"],
+                                 "TFLOPs": pf["flops"] / (pf["us_per_layer"] * 1e-6) / 1e12}}
+    e2e = bench_e2e(dev)
+    return {"decode_e2e_cfg5": {str(k): v for k, v in e2e.items()}}
+
+
 def main():
     args = _args()
     if args.traffic_from:
@@ -679,6 +709,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.pmc_sample:
         pmc_sample(dev)
+        return
+    if args.only:
+        print(json.dumps(_only(args.only, args.steps, args.warmup, dev)), flush=True)
         return
     if args.prefill_only:
         pf = bench_prefill(args.steps, args.warmup, dev)

@@ -75,6 +75,31 @@ def test_config2_ragged_24_layers(dev, use_kv_last):
     assert worst <= TOL
 
 
+@pytest.mark.parametrize("batch,length", [(1, 8192), (2, 4096), (4, 8192), (8, 2048), (8, 4096),
+                                          (3, 5000)])
+def test_decode_plan_shapes_match_oracle(dev, batch, length):
+    """The default plan (ops.decode_plan) at the shapes where it picks split +
+    combine launches with 32-128 splits or a capped single launch; rows
+    ragged through kv_last, stale NaN past each row's last slot."""
+    case = workloads.decode_uniform(batch, length, seed=length + batch)
+    gen = torch.Generator().manual_seed(batch)
+    lengths = torch.randint(length // 2, length + 1, (batch,), generator=gen).tolist()
+    for b, n in enumerate(lengths):
+        case.key_cache[b, :, n:] = float("nan")
+        case.value_cache[b, :, n:] = float("nan")
+    kv_last = torch.tensor([n - 1 for n in lengths], dtype=torch.int64, device=dev)
+    splits, fused = ops.decode_plan(batch, 2, length)
+    print(f"[decode plan B={batch} L={length}] splits={splits} fused={fused}", flush=True)
+    out, flash = _run(case, dev, kv_last=kv_last)
+    assert flash[0].shape[2] == splits and (len(flash) > 4) == fused
+    worst = 0.0
+    for b, n in enumerate(lengths):
+        ref = oracle.grouped_decode_attention(case.grouped[b:b + 1], case.key_cache[b:b + 1, :, :n],
+                                              case.value_cache[b:b + 1, :, :n], None)
+        worst = max(worst, _err(out[b:b + 1], ref))
+    assert worst <= TOL
+
+
 def test_partials_match_oracle_split(dev):
     case = workloads.decode_ragged(4, seed=3)
     splits = 7
