@@ -149,116 +149,72 @@ __device__ __forceinline__ void lse_merge_lanes(float& M, float& L, f32x4& A) {
   A = a0;
 }
 
-// Folds partials j = j0, j0 + step, ... (< S) of (b, h) = bh, query q, dims
-// 4*d4 .. +3 into the running state (M, L, A), eight partials per batch with
-// every load of a batch issued before the first use.  The loads are buffer
-// loads bounded to this (b, h)'s partials: slots past S read 0 and get weight
-// 0.  kCoherent: sc1 loads, for partials written by other workgroups of the
-// same launch with sc1 stores.
-template <bool kCoherent>
-__device__ __forceinline__ void fold_partials(const DecodeArgs& a, int bh, int q, int d4, int j0,
-                                              int step, float& M, float& L, f32x4& A) {
+// Folds partials of query q of (b, h) = bh into the running state (M, L, A)
+// of dims 4*d4 .. +3, d4 = lane % 16.  The wave's four 16-lane rows hold the
+// consecutive subs sub0 + lane / 16 out of nsub; sub folds partials
+// j = sub + nsub * u, batch after batch of kB (j < S).  In a batch the wave
+// loads each of its 4 kB partials' (m, l) once -- lane i loads partial
+// sub0 + i % 4 + nsub * (i / 4) -- and hands them to the 16 lanes that fold
+// the partial with ds_bpermute; the acc slices are one 16-byte load per lane
+// and partial, at a uniform distance (scalar offset) from the first.  So a
+// batch is 2 + kB vector memory instructions per wave, all in flight before
+// the first wait: one round trip.  (Sixteen lanes loading each (m, l) would
+// make it 2 kB more, and the merge is bound by those instructions.)
+// kCoherent: sc1 loads, for partials that other workgroups of the same
+// launch stored with sc1 stores.
+template <int kB, bool kCoherent>
+__device__ __forceinline__ void fold_wave(const DecodeArgs& a, int bh, int q, int lane, int sub0,
+                                          int nsub, float& M, float& L, f32x4& A) {
+  static_assert(4 * kB <= 64, "a batch's (m, l) must fit one load per lane");
   const int G = a.G, S = a.splits;
-  const int64_t pbase = (int64_t)bh * S;
+  const int s4 = lane >> 4, d4 = lane & 15, sub = sub0 + s4;
   constexpr int aux = kCoherent ? kSc1 : 0;
+  const int64_t pbase = (int64_t)bh * S;
   const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a.acc + pbase * G * kD, (int64_t)S * G * kD * 4);
   const __amdgpu_buffer_rsrc_t rm = buffer_rsrc(a.m + pbase * G, (int64_t)S * G * 4);
   const __amdgpu_buffer_rsrc_t rl = buffer_rsrc(a.l + pbase * G, (int64_t)S * G * 4);
-  // Partial u of a batch sits a uniform distance past partial 0: the lane's
-  // offsets are computed once per batch and u's distance goes in the
-  // scalar offset, so a batch costs registers for its data only.
-  constexpr int kBatch = 8;
-  const int ml_step = step * G * 4, acc_step = step * G * kD * 4;
-  for (; j0 < S; j0 += kBatch * step) {
-    const int row0 = j0 * G + q;
-    const int ml_off = row0 * 4, acc_off = (row0 * kD + 4 * d4) * 4;
-    float mv[kBatch], lv[kBatch];
-    f32x4 av[kBatch];
+  const int ml_lane = lane < 4 * kB ? lane : 0;
+  const int j_ml = sub0 + (ml_lane & 3) + nsub * (ml_lane >> 2);
+  const int acc_step = nsub * G * kD * 4;
+  for (int j0 = 0; j0 < S; j0 += nsub * kB) {
+    // Partials past S read 0 (the buffers end there) and are masked below.
+    const float m_mine = __builtin_bit_cast(
+        float, __builtin_amdgcn_raw_buffer_load_b32(rm, ((j0 + j_ml) * G + q) * 4, 0, aux));
+    const float l_mine = __builtin_bit_cast(
+        float, __builtin_amdgcn_raw_buffer_load_b32(rl, ((j0 + j_ml) * G + q) * 4, 0, aux));
+    const int acc_off = (((j0 + sub) * G + q) * kD + 4 * d4) * 4;
+    f32x4 av[kB];
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
+    for (int u = 0; u < kB; ++u)
       av[u] = __builtin_bit_cast(
           f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, acc_off, u * acc_step, aux));
-      mv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rm, ml_off, u * ml_step, aux));
-      lv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rl, ml_off, u * ml_step, aux));
-    }
     // Keep every load of the batch above this point: left alone, the
-    // scheduler sinks loads next to their uses to save registers, and the
-    // batch becomes a chain of dependent round trips.
+    // scheduler sinks loads next to their uses, and the batch becomes a chain
+    // of dependent round trips.
     __builtin_amdgcn_sched_barrier(0);
+    float mv[kB], lv[kB];
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u)
-      if (j0 + step * u >= S) mv[u] = kNegInf;
+    for (int u = 0; u < kB; ++u) {
+      mv[u] = __shfl(m_mine, s4 + 4 * u);
+      lv[u] = __shfl(l_mine, s4 + 4 * u);
+      if (j0 + sub + nsub * u >= S) mv[u] = kNegInf;
+    }
     float mc = mv[0];
 #pragma unroll
-    for (int u = 1; u < kBatch; ++u) mc = fmaxf(mc, mv[u]);
+    for (int u = 1; u < kB; ++u) mc = fmaxf(mc, mv[u]);
     const float mn = fmaxf(M, mc);
     const float safe = (mn == kNegInf) ? 0.f : mn;
     const float r = (M == kNegInf) ? 0.f : fast_exp2((M - safe) * kLog2e);
     L *= r;
     A *= r;
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
+    for (int u = 0; u < kB; ++u) {
       const float wu = (mv[u] == kNegInf) ? 0.f : fast_exp2((mv[u] - safe) * kLog2e);
       L += wu * lv[u];
       A += wu * av[u];
     }
     M = mn;
   }
-}
-
-// Single-launch merge of query q of (b, h) = bh by one wave: lane
-// (sub = lane / 16, d4 = lane % 16) folds partials j = sub + 4u (u < kB,
-// j < S <= 4 kB) of dims 4*d4 .. +3 into (M, L, A).  Each partial's (m, l)
-// is loaded once per wave -- lane j loads partial j's -- and handed to the
-// folding lanes with ds_bpermute, so a wave issues 2 + kB vector memory
-// instructions (the m/l loads of the 16 lanes that share a partial would
-// otherwise be 16 identical requests each), all before the first wait: one
-// round trip.  sc1 loads: the partials come from other workgroups' sc1
-// stores.
-template <int kB>
-__device__ __forceinline__ void merge_query(const DecodeArgs& a, int bh, int q, int lane, float& M,
-                                            float& L, f32x4& A) {
-  const int G = a.G, S = a.splits;
-  const int sub = lane >> 4, d4 = lane & 15;
-  const int64_t pbase = (int64_t)bh * S;
-  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a.acc + pbase * G * kD, (int64_t)S * G * kD * 4);
-  const __amdgpu_buffer_rsrc_t rm = buffer_rsrc(a.m + pbase * G, (int64_t)S * G * 4);
-  const __amdgpu_buffer_rsrc_t rl = buffer_rsrc(a.l + pbase * G, (int64_t)S * G * 4);
-  // Lanes >= S read past the partials: the buffer returns 0 (masked below).
-  const float m_mine = __builtin_bit_cast(
-      float, __builtin_amdgcn_raw_buffer_load_b32(rm, (lane * G + q) * 4, 0, kSc1));
-  const float l_mine = __builtin_bit_cast(
-      float, __builtin_amdgcn_raw_buffer_load_b32(rl, (lane * G + q) * 4, 0, kSc1));
-  const int acc_off = ((sub * G + q) * kD + 4 * d4) * 4, acc_step = 4 * G * kD * 4;
-  f32x4 av[kB];
-#pragma unroll
-  for (int u = 0; u < kB; ++u)
-    av[u] = __builtin_bit_cast(
-        f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, acc_off, u * acc_step, kSc1));
-  __builtin_amdgcn_sched_barrier(0);  // every load above is in flight before the first wait
-  float mv[kB], lv[kB];
-#pragma unroll
-  for (int u = 0; u < kB; ++u) {
-    const int j = sub + 4 * u;
-    mv[u] = __shfl(m_mine, j);
-    lv[u] = __shfl(l_mine, j);
-    if (j >= S) mv[u] = kNegInf;
-  }
-  float mn = mv[0];
-#pragma unroll
-  for (int u = 1; u < kB; ++u) mn = fmaxf(mn, mv[u]);
-  const float safe = (mn == kNegInf) ? 0.f : mn;
-  float Ls = 0.f;
-  f32x4 As = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int u = 0; u < kB; ++u) {
-    const float wu = (mv[u] == kNegInf) ? 0.f : fast_exp2((mv[u] - safe) * kLog2e);
-    Ls += wu * lv[u];
-    As += wu * av[u];
-  }
-  M = mn;
-  L = Ls;
-  A = As;
 }
 
 // fp16 out[b, h, q, 4*d4 .. +3] = A / L.
@@ -558,7 +514,7 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     // loads), so it reads the stored values.  It merges all S partials --
     // wave w takes queries w, w + NW, ...; within a wave lane
     // (sub = lane / 16, d4 = lane % 16) folds partials j = sub (mod 4)
-    // (merge_query) and the four subs merge through permlane swaps -- then
+    // (fold_wave) and the four subs merge through permlane swaps -- then
     // re-arms the ticket.
     int32_t* tk = a.ticket + bh;
     s_waitcnt_vm(0);
@@ -569,9 +525,8 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     for (int q = w; q < G; q += NW) {
       float Mq = kNegInf, Lq = 0.f;
       f32x4 Aq = {0.f, 0.f, 0.f, 0.f};
-      if (S <= 16) merge_query<4>(a, bh, q, lane, Mq, Lq, Aq);
-      else if (S <= 32) merge_query<8>(a, bh, q, lane, Mq, Lq, Aq);
-      else fold_partials<true>(a, bh, q, lane & 15, lane >> 4, 4, Mq, Lq, Aq);
+      if (S <= 16) fold_wave<4, true>(a, bh, q, lane, 0, 4, Mq, Lq, Aq);
+      else fold_wave<8, true>(a, bh, q, lane, 0, 4, Mq, Lq, Aq);
       lse_merge_lanes<false>(Mq, Lq, Aq);
       lse_merge_lanes<true>(Mq, Lq, Aq);
       if (lane < 16) store_out(a, bh, q, lane, Lq, Aq);
@@ -582,17 +537,17 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
 
 // Second launch of the two-kernel shape: one workgroup of four waves per
 // (b, h, query).  Thread (sub = tid / 16, d4 = tid % 16) folds partials
-// j = sub, sub + 16, ... of dims 4*d4 .. +3, with all loads of a batch of
-// eight issued before use; the 4 subs of a wave merge through permlane swaps
-// (lanes d4 + 16r), the 4 waves through LDS, and wave 0 writes fp16 acc / l.
+// j = sub, sub + 16, ... of dims 4*d4 .. +3 (fold_wave, eight per batch);
+// the 4 subs of a wave merge through permlane swaps (lanes d4 + 16r), the 4
+// waves through LDS, and wave 0 writes fp16 acc / l.
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
   __shared__ float red[3][16][6];
   const int bh = blockIdx.x / a.G, q = blockIdx.x % a.G;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int d4 = lane & 15, sub = tid >> 4;
+  const int d4 = lane & 15;
   float M = kNegInf, L = 0.f;
   f32x4 A = {0.f, 0.f, 0.f, 0.f};
-  fold_partials<false>(a, bh, q, d4, sub, 16, M, L, A);
+  fold_wave<8, false>(a, bh, q, lane, 4 * w, 16, M, L, A);
   lse_merge_lanes<false>(M, L, A);
   lse_merge_lanes<true>(M, L, A);
   if (w > 0 && lane < 16) {
