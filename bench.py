@@ -362,6 +362,41 @@ def hbm_copy_ceiling(dev, mib=512, reps=20):
     return 2 * src.numel() * 2 / (ms * 1e-3) / 1e9
 
 
+def hbm_read_ceiling(dev, sizes_mib=(16, 256), workgroups=(512, 1024, 2048, 4096)):
+    """Read-only HBM rate (qf_stream_read: 16-byte loads, grid-stride) at the
+    config-3 size and the bandwidth-regime size, over buffers rotated past the
+    MALL (at least 512 MiB per pass), best over a few workgroup counts."""
+    import torch
+
+    from qwenforge_amd import _lib
+
+    lib = _lib.load()
+    sink = torch.zeros(4 * max(workgroups), device=dev, dtype=torch.int32)
+    out = {}
+    for mib in sizes_mib:
+        nbuf = max(2, -(-512 // mib))
+        bufs = [torch.empty(mib << 18, device=dev, dtype=torch.int32).fill_(i) for i in range(nbuf)]
+        best = None
+        for wg in workgroups:
+            def run(wg=wg):
+                for b in bufs:
+                    _lib.check(lib.qf_stream_read(b.data_ptr(), mib << 20, sink.data_ptr(), wg,
+                                                  torch.cuda.current_stream().cuda_stream),
+                               "qf_stream_read")
+            ms = _time_graphs([GraphStep(run)], 10, 2) / nbuf
+            gbs = (mib << 20) / (ms * 1e-3) / 1e9
+            if best is None or gbs > best[0]:
+                best = (gbs, wg, ms)
+        out[f"{mib}MiB"] = {"GBps": round(best[0], 1), "us": round(best[2] * 1e3, 2),
+                            "workgroups": best[1], "frac_of_peak": round(best[0] / HBM_PEAK_GBS, 4)}
+        del bufs
+        torch.cuda.empty_cache()
+    out["what"] = ("qf_stream_read (include/qf_probe.h): read-only 16-byte loads, "
+                   f"{nbuf}+ buffers rotated per graph so reads miss the MALL; best of "
+                   f"{list(workgroups)} workgroups")
+    return out
+
+
 def bench_prefill(steps, warmup, dev, seq=2048):
     """Config 4: causal prefill S=2048 with fused RoPE + cache append (other
     lengths for the long-prompt leg)."""
@@ -830,6 +865,7 @@ def main():
         line["hbm_copy_ceiling"] = {"GBps": round(copy_gbs, 1),
                                     "frac_of_peak": round(copy_gbs / HBM_PEAK_GBS, 4),
                                     "what": "torch copy_ of 512 MiB, read + write bytes / time"}
+        line["hbm_read_ceiling"] = hbm_read_ceiling(dev)
         pf = bench_prefill(args.steps, args.warmup, dev)
         tf = pf["flops"] / (pf["us_per_layer"] * 1e-6) / 1e12
         line["prefill_cfg4"] = {

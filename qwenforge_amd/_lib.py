@@ -1,5 +1,5 @@
-"""ctypes binding of the C ABI in ``include/qf_attn.h``, ``include/qf_step.h`` and
-``include/qf_paged.h``.
+"""ctypes binding of the C ABI in ``include/qf_attn.h``, ``include/qf_step.h``,
+``include/qf_paged.h`` and ``include/qf_probe.h``.
 
 The shared object is built in-tree by ``qwenforge_amd.build``.  There is no
 fallback: if it is missing or does not load, every op raises.
@@ -212,6 +212,8 @@ SIGNATURES = {
         _i32, _i32, _i32,               # N, K, layout
         _vp,                            # stream
     ],
+    # include/qf_probe.h
+    "qf_stream_read": [_vp, _i64, _vp, _i32, _vp],   # src, bytes, sink, workgroups, stream
     "qf_error_string": [_i32],
     "qf_abi_version": [],
 }

@@ -77,6 +77,14 @@ def test_decode_launch_plan_names_the_kernel():
     assert _lib.load().qf_decode_waves(1, 2, 0, 512, 1, 0) == -1
 
 
+def test_stream_read_rejects_bad_arguments():
+    lib = _lib.load()
+    assert lib.qf_stream_read(None, 1024, 16, 4, None) == -1
+    assert lib.qf_stream_read(16, 1000, 16, 4, None) == -1   # not a multiple of 16 bytes
+    assert lib.qf_stream_read(8, 1024, 16, 4, None) == -1    # misaligned source
+    assert lib.qf_stream_read(16, 1024, 16, 0, None) == -1
+
+
 def test_noalloc_decode_rejects_before_any_hip_call():
     """Shape, size and pointer checks of qf_decode_attn_noalloc return before the
     library touches the device (no GPU here)."""
