@@ -228,9 +228,12 @@ __device__ __forceinline__ void store_out(const DecodeArgs& a, int bh, int q, in
 
 enum Bias { kNoBias = 0, kBiasVec = 1, kBiasScalar = 2 };
 
+// The V rows are kept as raw 32-bit words (two dims each): as f16 vectors
+// the compiler splits them into 16-bit pieces across the tile loop's back
+// edge, which puts unpacking (and a wait) right behind every load.
 struct Tile {
   f16x8 k[2][2];  // [score block j][k step kk]
-  f16x8 v[4];     // 4 keys x 8 dims
+  u32x4 v[4];     // 4 keys x 8 dims
   f16x8 bias;     // bias of the lane's keys t0 + 8*grp .. +7
 };
 
@@ -261,7 +264,7 @@ __device__ __forceinline__ void load_tile(Tile& t, const f16* kb, const f16* vb,
   for (int r = 0; r < 4; ++r) {
     int key = t0 + m4 + r;
     key = key < last ? key : last;
-    t.v[r] = load16(vb + (int64_t)key * v_sn + c8);
+    t.v[r] = __builtin_bit_cast(u32x4, load16(vb + (int64_t)key * v_sn + c8));
   }
   const int kbase = t0 + 8 * grp;
   if (kBias == kBiasVec) {
@@ -284,12 +287,10 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
   constexpr bool kHasBias = kBias != kNoBias;
   constexpr int NT = NW * 64;
   constexpr bool kCoh = kMode == kFused;
-  // LDS: per-wave transposed V tiles during the sweep, reused for the
-  // cross-wave merge and the split merges afterwards.
+  // LDS: per-wave transposed V tiles during the sweep; each wave's region
+  // then holds that wave's accumulator for the cross-wave merge.
   constexpr int kVtBytes = NW * kD * kVtStride * 2;
-  constexpr int kWaveMergeBytes = NW * 4 * 64 * 16;
-  constexpr int kLdsBytes = kVtBytes > kWaveMergeBytes ? kVtBytes : kWaveMergeBytes;
-  __shared__ __attribute__((aligned(16))) unsigned char lds_raw[kLdsBytes];
+  __shared__ __attribute__((aligned(16))) unsigned char lds_raw[kVtBytes];
   __shared__ float sm_ml[2][NW][kMaxG];
   __shared__ int sh_last;
 
@@ -357,22 +358,16 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
   };
 
   const int last = hi - 1;
-  int t0 = lo + w * kTile;
-  Tile cur, nxt;
+  constexpr int kStep = NW * kTile;
   const f16 *kt_, *vt_;
-  if (kPaged && t0 < hi) load_pids(0, last);
-  if (t0 < hi) {
-    tile_base(0, t0, kt_, vt_);
-    load_tile<kBias>(cur, kt_, vt_, biasb, a.k_sn, a.v_sn, t0, last, a.cap, lane);
-  }
-  for (int i = 0; t0 < hi; t0 += NW * kTile, ++i) {
-    const int tn = t0 + NW * kTile;
-    if (tn < hi) {
-      if (kPaged && ((i + 1) & 63) == 0) load_pids(i + 1, last);
-      tile_base(i + 1, tn, kt_, vt_);
-      load_tile<kBias>(nxt, kt_, vt_, biasb, a.k_sn, a.v_sn, tn, last, a.cap, lane);
-    }
-
+  // Issues the loads of the wave's tile i (first key tn) into t.
+  const auto prefetch = [&](Tile& t, int i, int tn) __attribute__((always_inline)) {
+    if (kPaged && (i & 63) == 0) load_pids(i, last);
+    tile_base(i, tn, kt_, vt_);
+    load_tile<kBias>(t, kt_, vt_, biasb, a.k_sn, a.v_sn, tn, last, a.cap, lane);
+  };
+  // Scores, online softmax and PV product of one tile (keys t0 .. t0 + 31).
+  const auto consume = [&](const Tile& cur, int t0) __attribute__((always_inline)) {
     // Bias of the lane's 8 keys t0 + 8*grp + jj, in log2 units.
     float bv[8];
     const int kbase = t0 + 8 * grp;
@@ -388,12 +383,16 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     c1 = mfma16x16x32(cur.k[1][1], qf[1], c1);
 
     // Transpose V into LDS: vt[d][key - t0], four keys per 8-byte write.
+    // Dim e of the four keys: the low (e even) or high half of word e / 2 of
+    // each row, paired by byte selects.
     {
       const int m4 = 4 * (lane & 7), c8 = 8 * (lane >> 3);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        f16x4 col4 = {cur.v[0][e], cur.v[1][e], cur.v[2][e], cur.v[3][e]};
-        *reinterpret_cast<f16x4*>(&vt[c8 + e][m4]) = col4;
+        const unsigned sel = (e & 1) ? 0x07060302u : 0x05040100u;
+        const u32x2 w = {__builtin_amdgcn_perm(cur.v[1][e >> 1], cur.v[0][e >> 1], sel),
+                         __builtin_amdgcn_perm(cur.v[3][e >> 1], cur.v[2][e >> 1], sel)};
+        *reinterpret_cast<f16x4*>(&vt[c8 + e][m4]) = __builtin_bit_cast(f16x4, w);
       }
     }
 
@@ -431,76 +430,113 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
       o[t] = mfma16x16x32(va, pb, o[t] * resc);
     }
     __builtin_amdgcn_wave_barrier();
-    cur = nxt;
+  };
+  // Two tile buffers in turn.  The wave's tile count n is known up front, so
+  // the loop runs whole pairs whose prefetches are unconditional and the one
+  // or two remaining tiles are peeled: no load batch sits behind a branch and
+  // no two paths with different loads in flight meet, so the compiler's wait
+  // before each use counts exactly the newer tile's loads as still in flight
+  // and two tiles are in flight while the older one lands.  (With a
+  // conditional prefetch the waits had to cover every load, the prefetch
+  // included, so a tile's compute could not overlap the next tile's loads.)
+  // The scheduling barriers keep each tile's first use below the next tile's
+  // loads.
+  int t0 = lo + w * kTile;
+  const int n = t0 < hi ? (hi - t0 + kStep - 1) / kStep : 0;
+  if (n > 0) {
+    Tile ta, tb;
+    prefetch(ta, 0, t0);
+    int i = 0;
+    for (; i + 2 < n; i += 2, t0 += 2 * kStep) {
+      prefetch(tb, i + 1, t0 + kStep);
+      __builtin_amdgcn_sched_barrier(0);
+      consume(ta, t0);
+      prefetch(ta, i + 2, t0 + 2 * kStep);
+      __builtin_amdgcn_sched_barrier(0);
+      consume(tb, t0 + kStep);
+    }
+    if (i + 2 == n) {
+      prefetch(tb, i + 1, t0 + kStep);
+      __builtin_amdgcn_sched_barrier(0);
+      consume(ta, t0);
+      consume(tb, t0 + kStep);
+    } else {
+      consume(ta, t0);
+    }
   }
 
   l_run = col_sum(l_run);
 
-  // Cross-wave merge.  A wave's softmax state is replicated over the four
-  // lanes of each query column.  The waves exchange (m, l) per column; each
-  // wave then scales its accumulator by exp2(m_w - M) and writes it to LDS as
-  // 16-byte rows [w][t][lane]; wave w' < min(NW, 4) sums the NW rows of its
-  // 16-dim slices t = w', w' + NW, ... and stores them from the MFMA layout
-  // (lane (q, grp) holds dims 16t + 4grp .. +3 of query q).  Two barriers;
-  // each LDS pass is one round of independent accesses.
-  // Only the first nact waves saw a tile (the split is shorter than NW
-  // tiles, e.g. when the single-launch merge asks for a wave per query):
-  // the others hold an empty state and take no part in the exchange.
-  int nact = (hi - lo + kTile - 1) / kTile;
-  nact = nact < 1 ? 1 : (nact > NW ? NW : nact);
+  // Cross-wave merge, one barrier.  A wave's softmax state is replicated over
+  // the four lanes of each query column.  Every wave publishes its (m, l) per
+  // column and its unscaled accumulator as 16-byte rows [t][lane] in its own
+  // V-tile region of LDS (no other wave touches that region, so no barrier
+  // is needed before the overwrite); a wave that saw no tile publishes the
+  // empty state (m = -inf, l = 0, zero accumulator), which drops out of the
+  // merge.  After the barrier wave w' < min(NW, 4) merges (M, L) and sums the
+  // NW accumulators of its 16-dim slices t = w', w' + NW, ..., each scaled by
+  // exp2(m_w - M), and stores them from the MFMA layout (lane (q, grp) holds
+  // dims 16t + 4grp .. +3 of query q).  Every LDS read of the pass is
+  // independent of the others.
+  constexpr int kWaveLds = kD * kVtStride * 2;  // bytes of a wave's V tile
+  static_assert(4 * 64 * 16 <= kWaveLds, "a wave's accumulator fits its V-tile region");
+  const auto sm_o = [&](int ww) { return reinterpret_cast<f32x4*>(lds_raw + ww * kWaveLds); };
   if (grp == 0) {
     sm_ml[0][w][col] = m_run;
     sm_ml[1][w][col] = l_run;
   }
-  __syncthreads();  // (m, l) visible; every wave is done with its V tiles
-  float M = kNegInf;
+  // The V-tile reads above and the f32 writes below alias the same bytes
+  // through different types: keep the compiler from reordering them (the
+  // wave's LDS accesses then execute in program order).
+  asm volatile("" ::: "memory");
 #pragma unroll
-  for (int ww = 0; ww < NW; ++ww)
-    if (ww < nact) M = fmaxf(M, sm_ml[0][ww][col]);
-  const float safe = (M == kNegInf) ? 0.f : M;
-  float L = 0.f;
-#pragma unroll
-  for (int ww = 0; ww < NW; ++ww) {
-    if (ww >= nact) break;
-    const float mw = sm_ml[0][ww][col];
-    L += ((mw == kNegInf) ? 0.f : fast_exp2(mw - safe)) * sm_ml[1][ww][col];
-  }
-  const float wt = (m_run == kNegInf) ? 0.f : fast_exp2(m_run - safe);
-  f32x4* sm_o = reinterpret_cast<f32x4*>(lds_raw);  // [NW][4][64]
-  if (w < nact) {
-#pragma unroll
-    for (int t = 0; t < 4; ++t) sm_o[(w * 4 + t) * 64 + lane] = o[t] * wt;
-  }
+  for (int t = 0; t < 4; ++t) sm_o(w)[t * 64 + lane] = o[t];
   __syncthreads();
 
   const int S = a.splits, G = a.G;
   const int64_t part = (int64_t)bh * S + s;
-  for (int t = w; t < 4; t += NW) {
-    f32x4 acc = sm_o[t * 64 + lane];
+  if (w < 4) {
+    float mw[NW], wt[NW];
+    float M = kNegInf;
 #pragma unroll
-    for (int ww = 1; ww < NW; ++ww)
-      if (ww < nact) acc += sm_o[(ww * 4 + t) * 64 + lane];
-    if (col < G) {
-      const int d = 16 * t + 4 * grp;
-      if (kMode == kDirect) {
-        const float inv = 1.f / L;
-        const f16x4 ov = {(f16)(acc[0] * inv), (f16)(acc[1] * inv), (f16)(acc[2] * inv),
-                          (f16)(acc[3] * inv)};
-        *reinterpret_cast<f16x4*>(a.out + b * a.o_sb + h * a.o_sh + col * a.o_sg + d) = ov;
-      } else if (kCoh) {
-        // The resource must be wave-uniform (it lives in SGPRs): one per
-        // split, the lane's query row and dims go in the offset.
-        const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a.acc + part * G * kD, (int64_t)G * kD * 4);
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc), ra,
-                                               (col * kD + d) * 4, 0, kSc1);
-      } else {
-        *reinterpret_cast<f32x4*>(a.acc + (part * G + col) * kD + d) = acc;
+    for (int ww = 0; ww < NW; ++ww) {
+      mw[ww] = sm_ml[0][ww][col];
+      M = fmaxf(M, mw[ww]);
+    }
+    const float safe = (M == kNegInf) ? 0.f : M;
+    float L = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) {
+      wt[ww] = (mw[ww] == kNegInf) ? 0.f : fast_exp2(mw[ww] - safe);
+      L += wt[ww] * sm_ml[1][ww][col];
+    }
+    for (int t = w; t < 4; t += NW) {
+      f32x4 acc = sm_o(0)[t * 64 + lane] * wt[0];
+#pragma unroll
+      for (int ww = 1; ww < NW; ++ww) acc += sm_o(ww)[t * 64 + lane] * wt[ww];
+      if (col < G) {
+        const int d = 16 * t + 4 * grp;
+        if (kMode == kDirect) {
+          const float inv = 1.f / L;
+          const f16x4 ov = {(f16)(acc[0] * inv), (f16)(acc[1] * inv), (f16)(acc[2] * inv),
+                            (f16)(acc[3] * inv)};
+          *reinterpret_cast<f16x4*>(a.out + b * a.o_sb + h * a.o_sh + col * a.o_sg + d) = ov;
+        } else if (kCoh) {
+          // The resource must be wave-uniform (it lives in SGPRs): one per
+          // split, the lane's query row and dims go in the offset.
+          const __amdgpu_buffer_rsrc_t ra =
+              buffer_rsrc(a.acc + part * G * kD, (int64_t)G * kD * 4);
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc), ra,
+                                                 (col * kD + d) * 4, 0, kSc1);
+        } else {
+          *reinterpret_cast<f32x4*>(a.acc + (part * G + col) * kD + d) = acc;
+        }
       }
     }
-  }
-  if (kMode != kDirect && w == 0 && grp == 0 && col < G) {
-    st<kCoh>(a.m + part * G + col, (M == kNegInf) ? kNegInf : M * kLn2);
-    st<kCoh>(a.l + part * G + col, L);
+    if (kMode != kDirect && w == 0 && grp == 0 && col < G) {
+      st<kCoh>(a.m + part * G + col, (M == kNegInf) ? kNegInf : M * kLn2);
+      st<kCoh>(a.l + part * G + col, L);
+    }
   }
 
   if (kMode == kFused) {
