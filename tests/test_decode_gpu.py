@@ -144,14 +144,19 @@ def test_uniform_value_rows(dev):
     assert _err(out, row.float().expand_as(out)) <= 1e-3
 
 
-def test_kv_last_shared_equals_truncated_cache(dev):
+@pytest.mark.parametrize("splits,fused", [(None, None), (1, False), (3, True), (3, False),
+                                          (8, True), (33, True), (33, False)])
+def test_kv_last_shared_equals_truncated_cache(dev, splits, fused):
+    """2501 valid slots: 1 to 10 tiles per wave (odd and even counts of the
+    paired tile loop), with NaN in every slot past kv_last."""
     case = workloads.decode_uniform(1, 4096, seed=7)
     last = 2500
     kv_last = torch.tensor([last], dtype=torch.int64, device=dev)
     # Garbage past kv_last must never be read.
     case.key_cache[:, :, last + 1:] = float("nan")
     case.value_cache[:, :, last + 1:] = float("nan")
-    out, _ = _run(case, dev, kv_last=kv_last)
+    print(f"[decode kv_last splits={splits} fused={fused}]", flush=True)
+    out, _ = _run(case, dev, splits=splits, fused=fused, kv_last=kv_last)
     ref = oracle.grouped_decode_attention(case.grouped, case.key_cache[:, :, :last + 1],
                                           case.value_cache[:, :, :last + 1], None)
     assert _err(out, ref) <= TOL
