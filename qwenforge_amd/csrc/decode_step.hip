@@ -420,21 +420,18 @@ struct MergeArgs {
 template <int NB, int RW>
 __global__ __launch_bounds__(kNT) void attn_merge_gemv_residual_kernel(MergeArgs a) {
   constexpr int NS = kMaxNormK / 8 / 64;
+  // Splits folded per batch: the engine's split counts (8 at one row, 4 at
+  // more) in one batch, so the merge is one round trip.
+  constexpr int kSB = NB == 1 ? 8 : 4;
   __shared__ __attribute__((aligned(16))) f16 xs[NB * kMaxNormK];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int K = a.K, C = K / 8;
   const int n0 = (blockIdx.x * kNW + w) * RW;
-  const int re = lane < RW * NB ? lane / NB : 0, be = lane < RW * NB ? lane % NB : 0;
-  f16* hp = a.hidden + be * a.h_sb + min(n0 + re, a.N - 1);
-  const float resid = (float)*hp;
-  f16x8 wr[RW][NS];
-#pragma unroll
-  for (int r = 0; r < RW; ++r) load_row<NS>(a.w + (int64_t)min(n0 + r, a.N - 1) * K, C, wr[r], lane);
 
   // Merge: item = (b, h, g, 4 dims); xs offset of item `it` is 4 * it because
   // hidden index (h * G + g) * 64 + d matches the (B, KVH, G, D) output layout.
   // Thread t owns items t + kNT*i (i < NB covers NB * KVH * G * 16 <= NB * kNT
-  // items); each round loads four splits of every owned item at once.
+  // items); each batch loads kSB splits of every owned item at once.
   const int S = a.splits, G = a.G;
   const int items = NB * a.KVH * G * 16;
   float M[NB], L[NB];
@@ -451,30 +448,32 @@ __global__ __launch_bounds__(kNT) void attn_merge_gemv_residual_kernel(MergeArgs
     L[i] = 0.f;
     A[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  for (int s0 = 0; s0 < S; s0 += 4) {
-    float mv[NB][4], lv[NB][4];
-    f32x4 av[NB][4];
+  float mv[NB][kSB], lv[NB][kSB];
+  f32x4 av[NB][kSB];
+  const auto load_batch = [&](int s0) {
 #pragma unroll
     for (int i = 0; i < NB; ++i)
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < kSB; ++u) {
         const int64_t off = (int64_t)min(s0 + u, S - 1) * G;
         mv[i][u] = a.m[ml0[i] + off];
         lv[i][u] = a.l[ml0[i] + off];
         av[i][u] = reinterpret_cast<const f32x4*>(a.acc)[acc0[i] + off * 16];
       }
+  };
+  const auto fold_batch = [&](int s0) {
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       float mc = M[i];
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
+      for (int u = 0; u < kSB; ++u)
         if (s0 + u < S) mc = fmaxf(mc, mv[i][u]);
       const float safe = (mc == kNegInf) ? 0.f : mc;
       const float r = (M[i] == kNegInf) ? 0.f : fast_exp2((M[i] - safe) * kLog2e);
       L[i] *= r;
       A[i] *= r;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < kSB; ++u) {
         const float wt = (s0 + u >= S || mv[i][u] == kNegInf) ? 0.f
                                                                : fast_exp2((mv[i][u] - safe) * kLog2e);
         L[i] += wt * lv[i][u];
@@ -482,6 +481,25 @@ __global__ __launch_bounds__(kNT) void attn_merge_gemv_residual_kernel(MergeArgs
       }
       M[i] = mc;
     }
+  };
+  // The first batch of partials goes out before the weight rows: the partials
+  // are L2-resident and land first, so the merge runs while the weights are
+  // in flight (a wait for loads issued after the weights would wait for the
+  // weights too).
+  load_batch(0);
+  f16x8 wr[RW][NS];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) load_row<NS>(a.w + (int64_t)min(n0 + r, a.N - 1) * K, C, wr[r], lane);
+  const int re = lane < RW * NB ? lane / NB : 0, be = lane < RW * NB ? lane % NB : 0;
+  f16* hp = a.hidden + be * a.h_sb + min(n0 + re, a.N - 1);
+  const float resid = (float)*hp;
+  // Keep the loads above in flight together (left alone, the scheduler sinks
+  // them next to their uses).
+  __builtin_amdgcn_sched_barrier(0);
+  fold_batch(0);
+  for (int s0 = kSB; s0 < S; s0 += kSB) {
+    load_batch(s0);
+    fold_batch(s0);
   }
 #pragma unroll
   for (int i = 0; i < NB; ++i) {
