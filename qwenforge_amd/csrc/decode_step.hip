@@ -1196,6 +1196,7 @@ extern "C" int qf_gemv_residual(const void* inp, int64_t in_sb, const void* w, v
     if (ns <= 10) {
       if (B * C <= 4 * kNT) { QF_DISPATCH_B(B, gemv_residual_kernel, 10, 1, 4) }
       else if (B * C <= 8 * kNT) { QF_DISPATCH_B(B, gemv_residual_kernel, 10, 1, 8) }
+      else if (B * C <= 10 * kNT) { QF_DISPATCH_B(B, gemv_residual_kernel, 10, 1, 10) }
       else { QF_DISPATCH_B(B, gemv_residual_kernel, 10, 1, 16) }
     } else if (ns <= 12) {
       if (B * C <= 4 * kNT) { QF_DISPATCH_B(B, gemv_residual_kernel, 12, 1, 4) }
