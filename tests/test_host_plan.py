@@ -11,7 +11,10 @@ from qwenforge_amd import ops
 
 
 @pytest.mark.parametrize("batch,length,splits,fused", [
-    (1, 512, 8, True),       # config 1: 64-key splits, single launch
+    (1, 512, 16, True),      # config 1: 32-key splits, single launch (5.99 us vs 6.17 at 8)
+    (1, 2048, 16, True),     # 128-key splits: 6.70 us vs 7.04 at 32
+    (2, 512, 8, True),       # 6.23 us vs 6.58 at 4
+    (4, 512, 8, True),       # 6.55 us vs 6.70 at 4
     (4, 2048, 16, True),     # config 2 (cap 2048): 128-key splits, single launch
     (1, 32768, 128, False),  # config 3: split + combine
     (1, 4096, 32, True),     # <= 2 pairs and <= 4096 keys: single launch
