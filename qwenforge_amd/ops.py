@@ -79,7 +79,7 @@ def decode_plan(batch: int, kv_heads: int, length: int) -> tuple[int, bool]:
       12.2 us for 32 splits with the single-launch merge; B=8, L=8192: 13.2
       against 15.7).
 
-    More pairs keep the fill rule of ``_fill_splits``.  (The reference's
+    More pairs: one workgroup per CU (``_fill_splits``), single launch.  (The reference's
     rule, ``max(1, min(32, 272 // (B*KVH), cap // 256))`` at SE:1027, targets
     68 SMs and always uses two launches.)
     """
@@ -109,24 +109,16 @@ def _fill_splits(pairs: int, length: int, min_keys: int = 128,
     """Split count for more than 16 (b, kv head) pairs.
 
     The (split, b, kv-head) workgroups fill the CUs once -- floor(CUs / pairs)
-    splits -- or twice (two eight-wave workgroups share a CU) when that still
-    allows the single-launch merge (<= 32 splits) and keeps splits at <= 512
-    keys; where one per CU fills every CU exactly, twice only with splits of
-    >= 256 keys, and never when one split per row already fills the chip (no
-    merge at all).  A count just above one per CU leaves a few CUs with a
-    second workgroup and costs up to 30% (measured: B=12 L=5760 at 11 splits,
-    264 workgroups, 16.7 us vs 13.1 us at 10).  Splits are never shorter than
-    ``min_keys`` slots.  Measured on MI355X (B=12, L=5760: 21 splits, fused;
-    B=16, L=32768: 8, fused; B=64, L=4096: 2, fused).
+    splits -- never a count just above it (which leaves a few CUs with a
+    second workgroup: B=12 L=5760 at 11 splits, 264 workgroups, took 16.7 us
+    against 13.1 at 10).  Splits are never shorter than ``min_keys`` slots.
+    Measured on MI355X with the single-launch merge, one workgroup per CU
+    against two (twice the splits): B=12 L=5760 12.55 vs 13.35 us; B=16
+    L=4096 11.58 vs 13.13; B=10 L=4096 10.51 vs 11.94; B=12 L=2048 8.94 vs
+    9.99; B=24 L=2048 10.23 vs 10.97; B=12 L=8192 14.83 vs 15.81.
     """
     by_len = max(1, math.ceil(length / min_keys))
     s = max(1, target_workgroups // pairs)
-    s2 = 2 * target_workgroups // pairs
-    twice = 1 < s2 <= 32 and length <= 512 * s2
-    if twice and pairs * s == target_workgroups:
-        twice = s > 1 and length >= 256 * s2
-    if twice:
-        s = s2
     return max(1, min(by_len, s, 1024))
 
 

@@ -27,10 +27,10 @@ from qwenforge_amd import ops
     (8, 16384, 64, False),   # at most 1024 workgroups
     (16, 32768, 8, True),    # bandwidth regime: one workgroup per CU
     (64, 4096, 2, True),
-    (12, 5760, 21, True),    # the reference's benchmark shape: two per CU, fused
-    (20, 4096, 12, True),
+    (12, 5760, 10, True),    # the reference's benchmark shape: once per CU (12.55 vs 13.35 us at 21)
+    (20, 4096, 6, True),     # once per CU (12.86 vs 13.18 us at 12)
     (100, 4096, 1, False),   # 200 pairs: one split, no merge
-    (16, 4096, 16, True),    # exact fit, but 256-key splits: twice
+    (16, 4096, 8, True),     # exact fit, once per CU (11.58 vs 13.13 us at 16)
     (32, 1024, 4, True),
     (128, 1024, 1, False),   # 256 pairs: one split per row fills the chip, no merge
 ])
@@ -58,8 +58,8 @@ def test_workgroup_counts_stay_in_the_measured_ranges(batch):
             assert (wg <= 192) if fused else (full <= wg <= 4 * ops.NUM_CUS or s == 128), \
                 (batch, length, s)
         else:
-            # Once per CU, or twice with the single-launch merge.
-            assert wg <= ops.NUM_CUS or (s <= 32 and wg <= 2 * ops.NUM_CUS), (batch, length, s)
+            # Once per CU.
+            assert wg <= ops.NUM_CUS, (batch, length, s)
         # Splits keep at least one 32-key tile.
         assert -(-length // s) >= 32
 
