@@ -630,7 +630,10 @@ static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // small grids: at B=1 with 8 splits, 8 waves beat 16 by 0.7 us per call), four
 // for large grids -- and never more waves than the split has 32-key tiles
 // (idle waves only lengthen the cross-wave merge).  The single-launch merge
-// gives each query a wave: NW >= G.
+// gives each query a wave: NW >= G.  Otherwise (below 16 waves), down to
+// four waves, each wave gets at least two tiles, so its second tile's loads fly under the
+// first's compute (config 3, 8 tiles per split: 4 waves 10.57 us, 8 waves
+// 10.80).
 static int pick_waves(const DecodeArgs& a, int mode) {
   const int64_t wgs = (int64_t)a.splits * a.B * a.KVH;
   int nw = wgs <= 2 ? 16 : (wgs <= 512 ? 8 : 4);
@@ -638,6 +641,8 @@ static int pick_waves(const DecodeArgs& a, int mode) {
   const int tiles = (split_len + kTile - 1) / kTile;
   const int min_nw = mode == kFused ? a.G : 1;
   while (nw > 2 && nw / 2 >= tiles && nw / 2 >= min_nw) nw /= 2;
+  if (mode != kFused && wgs > 2)
+    while (nw > 4 && 2 * nw > tiles) nw /= 2;
   return nw;
 }
 
