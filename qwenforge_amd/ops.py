@@ -66,13 +66,15 @@ def decode_plan(batch: int, kv_heads: int, length: int) -> tuple[int, bool]:
     Up to 16 (b, kv head) pairs (measured on MI355X over 1-16 pairs and
     1024-32768 slots, every split count from 1 to 256 in both merge modes):
 
-    * short rows (``length <= 2048``, or ``<= 4096`` with at most 2 pairs):
-      the single-launch merge.  Up to 2048 slots and 8 pairs: splits of 32
-      keys (64 with more than 2 pairs), at most 16 -- e.g. config 1 (B=1,
-      L=512): 16 splits (5.99 us against 6.17 at 8); B=1, L=2048: 16 (6.70
-      against 7.04 at 32); config 2 (B=4, cap 2048): 16.  Otherwise splits
-      of about 128 keys (64 with at most 2 pairs), at most 32 splits and at
-      most 192 workgroups -- e.g. B=8, L=2048: 12; B=1, L=4096: 32;
+    * short rows (``length <= 2048``, or ``<= 4096`` with at most 8 pairs):
+      the single-launch merge.  Up to 2048 slots and 8 pairs, and 2049-4096
+      slots with 3-8 pairs: splits of 32 keys (64 with more than 2 pairs),
+      at most 16 -- e.g. config 1 (B=1, L=512): 16 splits (5.99 us against
+      6.17 at 8); B=1, L=2048: 16 (6.70 against 7.04 at 32); config 2 (B=4,
+      cap 2048): 16; B=4, L=4096: 16 (8.57 against 8.87 for 32 split +
+      combine).  Otherwise splits of about 128 keys (64 with at most 2
+      pairs), at most 32 splits and at most 192 workgroups -- e.g. B=8,
+      L=2048: 12; B=1, L=4096: 32;
     * longer rows: split + combine launches, splits of about 128 keys, at
       least 256 and at most 1024 workgroups, at most 128 splits -- e.g.
       config 3 (B=1, L=32768): 128; B=4, L=8192: 64 (10.9 us against
@@ -87,13 +89,13 @@ def decode_plan(batch: int, kv_heads: int, length: int) -> tuple[int, bool]:
     if pairs > 16:
         s = _fill_splits(pairs, length)
         return s, prefer_fused(s)
+    if pairs <= 8 and (length <= 2048 or (length <= 4096 and pairs > 2)):
+        keys = 32 if pairs <= 2 else 64
+        s = max(1, min(math.ceil(length / keys), 16))
+        return s, s > 1
     if length <= 2048 or (length <= 4096 and pairs <= 2):
-        if length <= 2048 and pairs <= 8:
-            keys = 32 if pairs <= 2 else 64
-            s = max(1, min(math.ceil(length / keys), 16))
-        else:
-            keys = 64 if pairs <= 2 else 128
-            s = max(1, min(math.ceil(length / keys), 192 // pairs, 32))
+        keys = 64 if pairs <= 2 else 128
+        s = max(1, min(math.ceil(length / keys), 192 // pairs, 32))
         return s, s > 1
     s = max(1, min(max(length // 128, NUM_CUS // pairs), 128, 4 * NUM_CUS // pairs))
     return s, False

@@ -19,8 +19,8 @@ from qwenforge_amd import ops
     (1, 32768, 128, False),  # config 3: split + combine
     (1, 4096, 32, True),     # <= 2 pairs and <= 4096 keys: single launch
     (1, 8192, 128, False),   # 8.6 us against 9.3 for 32 fused splits
-    (2, 4096, 64, False),
-    (4, 4096, 32, False),    # 9.5 us against 10.6
+    (2, 4096, 16, True),     # 7.82 us vs 8.07 for 64 split + combine
+    (4, 4096, 16, True),     # 8.57 us vs 8.87 for 32 split + combine
     (4, 8192, 64, False),    # 10.9 us against 12.2
     (8, 2048, 12, True),     # at most 192 workgroups with the single launch
     (8, 4096, 32, False),    # 11.0 us against 11.9
