@@ -31,9 +31,11 @@
 //             partial store is an agent-scope atomic store, so the completion
 //             wait is all an agent-scope release has to add here; the full
 //             release fence would also write back the whole L2 per workgroup.
-// Every merge is one pass of independent loads (eight partials per lane in
-// flight) followed by register / permlane / LDS reductions, so it costs one
-// dependent memory round trip.
+// Every merge folds its partials in batches of independent loads (four or
+// eight partials per lane, all in flight) followed by register / permlane /
+// LDS reductions: one dependent memory round trip per batch, and one batch
+// covers the single-launch merge's at most 32 splits and the combine's up to
+// 128.
 #include <mutex>
 
 #include "qf_common.h"
