@@ -3,8 +3,9 @@
 Its output must equal qf_decode_attn's (same kernels, same split count and
 merge; the existing entry point gets torch-allocated scratch) bit for bit, on
 two calls in a row where the second is smaller, for the single-launch merge
-(2-32 splits), the two-launch merge (> 32 splits) and one split; and stay
-within the 2e-3 max-abs-err of the CPU oracle.
+(2-32 splits), the two-launch merge (> 32 splits) and one split, and on four
+calls that change the layout and the merge in turn; and stay within the
+2e-3 max-abs-err of the CPU oracle.
 """
 
 import pytest
@@ -60,6 +61,12 @@ CASES = {
               (lambda: workloads.decode_uniform(1, 512, seed=4), 8, False)],
     "two_launch": [(lambda: workloads.decode_uniform(1, 32768, seed=5, heavy_frac=0.01), 128, False),
                    (lambda: workloads.decode_uniform(1, 4096, seed=6, cap=4160), 64, True)],
+    # Layout changes in both directions and between the merges: each call
+    # must find the partials the previous one used cleared.
+    "mixed": [(lambda: workloads.decode_uniform(2, 8192, seed=10), 64, False),
+              (lambda: workloads.decode_ragged(4, seed=11), 16, True),
+              (lambda: workloads.decode_uniform(2, 2048, seed=12), 32, False),
+              (lambda: workloads.decode_ragged(4, seed=13), 16, True)],
     "direct": [(lambda: workloads.decode_ragged(2, seed=7), 1, True),
                (lambda: workloads.decode_uniform(1, 100, seed=8, cap=128), 1, False)],
 }
