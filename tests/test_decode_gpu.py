@@ -227,6 +227,41 @@ def test_graph_capture_replay(dev):
         assert _err(got, ref) <= TOL, f"replay {step}"
 
 
+def test_single_launch_64_splits_graph_replay(dev):
+    """The single-launch merge past 32 splits (one workgroup folds all 64
+    partials of its (b, h)): captured once, replayed with new cache contents,
+    a moving kv_last and NaN past it; the tickets re-arm on every replay."""
+    case = workloads.decode_uniform(2, 8192, seed=13).to(dev)
+    flash = ops.make_flash_scratch(2, 2, 7, 8192, dev, splits=64, fused=True)
+    kv_last = torch.tensor([4000, 7000], dtype=torch.int64, device=dev)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ops.flash_decode_attention(case.grouped, case.key_cache, case.value_cache, None, flash, kv_last)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        ops.flash_decode_attention(case.grouped, case.key_cache, case.value_cache, None, flash, kv_last)
+    k0, v0 = case.key_cache.clone(), case.value_cache.clone()
+    for step, lasts in enumerate([(4000, 7000), (8191, 31), (2047, 2048), (100, 6000), (5000, 5000)]):
+        print(f"[decode 64-split replay {step}] kv_last={lasts}", flush=True)
+        kv_last.copy_(torch.tensor(lasts, dtype=torch.int64))
+        case.key_cache.copy_(k0)
+        case.value_cache.copy_(v0 * (-1 if step % 2 else 1))
+        for b, last in enumerate(lasts):
+            case.key_cache[b, :, last + 1:] = float("nan")
+            case.value_cache[b, :, last + 1:] = float("nan")
+        graph.replay()
+        torch.cuda.synchronize()
+        got = flash[3].float().cpu()
+        for b, last in enumerate(lasts):
+            ref = oracle.grouped_decode_attention(case.grouped[b:b + 1].cpu(),
+                                                  case.key_cache[b:b + 1, :, :last + 1].cpu(),
+                                                  case.value_cache[b:b + 1, :, :last + 1].cpu())
+            assert _err(got[b:b + 1], ref) <= TOL, f"replay {step} row {b}"
+    assert int(flash[4].abs().sum()) == 0
+
+
 def test_split_then_combine_equals_attn(dev):
     """The reference's two launches (SE:854-873) through the separate entry points."""
     case = workloads.decode_ragged(4, seed=21)
