@@ -118,7 +118,7 @@ def test_rms_qkv_gathers_embedding_rows_and_skips_out_of_range_slot(dev, tiles):
     assert not bool(kc.any()) and not bool(vc.any())  # slot == cap: nothing written
 
 
-@pytest.mark.parametrize("batch", [1, 4])
+@pytest.mark.parametrize("batch", [1, 2, 3, 4])
 @pytest.mark.parametrize("k_dim,n", [(HIDDEN, HIDDEN), (INTER, HIDDEN), (200, 72), (6144, 96),
                                      (8192, 64)])
 @pytest.mark.parametrize("integer", [True, False])
@@ -218,7 +218,7 @@ def test_lm_head_random_logits_close(dev):
     assert torch.equal(token.cpu(), logits.float().cpu().argmax(-1))
 
 
-@pytest.mark.parametrize("batch", [1, 4])
+@pytest.mark.parametrize("batch", [1, 2, 3, 4])
 @pytest.mark.parametrize("splits", [1, 5, 18])
 def test_attn_merge_o_proj(dev, batch, splits):
     """Split-K partials merged in the o_proj prologue == oracle attention + o_proj."""
