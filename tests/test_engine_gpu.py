@@ -25,8 +25,10 @@ def _fp32(w):
             "layers": [{k: v.float() for k, v in layer.items()} for layer in w["layers"]]}
 
 
-@pytest.mark.parametrize("batch", [1, 4])
+@pytest.mark.parametrize("batch", [1, 2, 3, 4, 6])
 def test_teacher_forced_logits_match_oracle(dev, batch):
+    """2 layers: the fused step at 1-4 rows (matrix-core tiles from 2), and at
+    6 rows the torch projections around the same attention kernels."""
     _teacher_forced(dev, Qwen2Config(layers=2), batch, 200, 6, (200 + 6 + 63) // 64 * 64)
 
 
