@@ -21,11 +21,11 @@
 // (b, h).  The waves merge through LDS.  Then, by mode:
 //   kDirect   (one split)  the workgroup writes the fp16 output itself;
 //   kPartial  it writes one partial (acc, m, l) in the reference's scratch
-//             layout and a second kernel merges them (the reference's
-//             two-launch shape);
-//   kFused    it writes the partial with write-through (sc1) stores, waits
-//             for them to complete (s_waitcnt vmcnt(0) in every wave, then a
-//             barrier) and takes the (b, h) ticket; the last workgroup of the
+//             layout, with write-through (sc1) stores, and a second kernel
+//             merges them (the reference's two-launch shape);
+//   kFused    it writes the partial likewise, waits for the stores to
+//             complete (s_waitcnt vmcnt(0) in every wave, then a barrier)
+//             and takes the (b, h) ticket; the last workgroup of the
 //             (b, h) merges all S partials (one wave per query) with sc1
 //             loads, writes the output and re-arms the ticket.  Every
 //             partial store is an agent-scope atomic store, so the completion
@@ -85,13 +85,11 @@ struct DecodeArgs {
   int log2p, n_pages;
 };
 
-// Partial-scratch stores.  kCoherent: a relaxed agent-scope atomic store,
-// which the compiler emits as a write-through (sc1) store, so a workgroup on
-// another XCD sees it without an L2 writeback.
-template <bool kCoherent>
-__device__ __forceinline__ void st(float* p, float v) {
-  if (kCoherent) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  else *p = v;
+// Partial-scratch store: a relaxed agent-scope atomic store, which the
+// compiler emits as a write-through (sc1) store, so a workgroup on another
+// XCD sees it without an L2 writeback.
+__device__ __forceinline__ void st_wt(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Slot range [lo, hi) of split `s` for batch row `b`: the row's valid slots
@@ -288,7 +286,6 @@ template <int NW, int kBias, int kMode, bool kPaged>
 __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
   constexpr bool kHasBias = kBias != kNoBias;
   constexpr int NT = NW * 64;
-  constexpr bool kCoh = kMode == kFused;
   // LDS: per-wave transposed V tiles during the sweep; each wave's region
   // then holds that wave's accumulator for the cross-wave merge.
   constexpr int kVtBytes = NW * kD * kVtStride * 2;
@@ -523,21 +520,24 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
           const f16x4 ov = {(f16)(acc[0] * inv), (f16)(acc[1] * inv), (f16)(acc[2] * inv),
                             (f16)(acc[3] * inv)};
           *reinterpret_cast<f16x4*>(a.out + b * a.o_sb + h * a.o_sh + col * a.o_sg + d) = ov;
-        } else if (kCoh) {
-          // The resource must be wave-uniform (it lives in SGPRs): one per
-          // split, the lane's query row and dims go in the offset.
+        } else {
+          // Partials are written through (sc1) in both merge modes: the
+          // single launch reads them from other XCDs, and before a combine
+          // launch they leave no dirty L2 lines for the end-of-kernel
+          // writeback (split + combine, B=1 L=32768: 10.16 vs 10.24 us;
+          // B=1 L=8192 8.03 vs 8.19).  The resource must be wave-uniform (it
+          // lives in SGPRs): one per split, the lane's query row and dims go
+          // in the offset.
           const __amdgpu_buffer_rsrc_t ra =
               buffer_rsrc(a.acc + part * G * kD, (int64_t)G * kD * 4);
           __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc), ra,
                                                  (col * kD + d) * 4, 0, kSc1);
-        } else {
-          *reinterpret_cast<f32x4*>(a.acc + (part * G + col) * kD + d) = acc;
         }
       }
     }
     if (kMode != kDirect && w == 0 && grp == 0 && col < G) {
-      st<kCoh>(a.m + part * G + col, (M == kNegInf) ? kNegInf : M * kLn2);
-      st<kCoh>(a.l + part * G + col, L);
+      st_wt(a.m + part * G + col, (M == kNegInf) ? kNegInf : M * kLn2);
+      st_wt(a.l + part * G + col, L);
     }
   }
 
