@@ -2,7 +2,8 @@
  * qf_probe.h -- calibration kernel for the roofline figures (no counterpart
  * in the reference; it is measurement infrastructure, not on the hot path).
  *
- *   qf_stream_read  reads `bytes` bytes at `src` with 16-byte loads spread over
+ *   qf_stream_read  reads `bytes` bytes at `src` with 16-byte non-temporal
+ *                   loads (the decode kernels' streaming flavor) spread over
  *                   `workgroups` workgroups (grid-stride) and writes one
  *                   uint32 per wave to `sink` (the XOR of what the wave
  *                   read), so the loads cannot be dropped.  `sink` holds

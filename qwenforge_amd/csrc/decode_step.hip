@@ -79,14 +79,16 @@ __device__ __forceinline__ f16x8 zero8() {
 // The NS 16-byte chunks of one weight row that lane `lane` multiplies:
 // chunk 64*s + lane, s < NS.  Lanes past the row's C chunks load its last
 // chunk (never used), so no load sits behind a branch and every load of a
-// wave is in flight at once.
+// wave is in flight at once.  A step reads each weight once, so the loads
+// are non-temporal (with the tile loads below, config 5 0.578 -> 0.526 ms
+// per step at B=1 and 0.726 -> 0.670 at B=4).
 template <int NS>
 __device__ __forceinline__ void load_row(const f16* __restrict__ w, int C, f16x8 (&r)[NS],
                                          int lane) {
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     const int c = min(64 * s + lane, C - 1);
-    r[s] = load16(w + 8 * c);
+    r[s] = load16_nt(w + 8 * c);
   }
 }
 
@@ -610,7 +612,7 @@ __global__ __launch_bounds__(kNT) void rms_gate_up_swiglu_kernel(GateUpArgs a) {
 // wave is one contiguous 1 KB read.  Tiles are stored rb-major.
 __device__ __forceinline__ f16x8 tile_load(const f16* __restrict__ w, int nkb, int rb, int kb,
                                            int lane) {
-  return load16(w + (((int64_t)rb * nkb + kb) * 64 + lane) * 8);
+  return load16_nt(w + (((int64_t)rb * nkb + kb) * 64 + lane) * 8);
 }
 
 // B operand of k block kb for lane l: staged activation row l % 16 at

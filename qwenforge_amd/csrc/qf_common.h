@@ -38,6 +38,12 @@ __device__ __forceinline__ f16x8 load16(const f16* p) {
   return *reinterpret_cast<const f16x8*>(p);
 }
 
+// 16-byte non-temporal load (the nt cache policy), for data a launch reads
+// exactly once: KV-cache tiles in decode, streamed weights.
+__device__ __forceinline__ f16x8 load16_nt(const f16* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const f16x8*>(p));
+}
+
 __device__ __forceinline__ void store16(f16* p, f16x8 v) {
   *reinterpret_cast<f16x8*>(p) = v;
 }
