@@ -63,23 +63,28 @@ def decode_plan(batch: int, kv_heads: int, length: int) -> tuple[int, bool]:
     """(split count, single-launch merge) for a decode call over rows of
     ``length`` slots on MI355X (256 CUs).
 
-    Up to 16 (b, kv head) pairs (measured on MI355X over 1-16 pairs and
-    1024-32768 slots, every split count from 1 to 256 in both merge modes):
+    Up to 16 (b, kv head) pairs (measured on MI355X, graph-replayed calls
+    over caches rotated past the MALL, every split count from 4 to 256 in both
+    merge modes at 1-8 rows and 512-32768 slots):
 
-    * short rows (``length <= 2048``, or ``<= 4096`` with at most 8 pairs):
-      the single-launch merge.  Up to 2048 slots and 8 pairs, and 2049-4096
-      slots with 3-8 pairs: splits of 32 keys (64 with more than 2 pairs),
-      at most 16 -- e.g. config 1 (B=1, L=512): 16 splits (5.99 us against
-      6.17 at 8); B=1, L=2048: 16 (6.70 against 7.04 at 32); config 2 (B=4,
-      cap 2048): 16; B=4, L=4096: 16 (8.57 against 8.87 for 32 split +
-      combine).  Otherwise splits of about 128 keys (64 with at most 2
-      pairs), at most 32 splits and at most 192 workgroups -- e.g. B=8,
-      L=2048: 12; B=1, L=4096: 32;
-    * longer rows: split + combine launches, splits of about 128 keys, at
-      least 256 and at most 1024 workgroups, at most 128 splits -- e.g.
-      config 3 (B=1, L=32768): 128; B=4, L=8192: 64 (10.9 us against
-      12.2 us for 32 splits with the single-launch merge; B=8, L=8192: 13.2
-      against 15.7).
+    * short rows (``length <= 2048`` with at most 8 pairs, or ``<= 512``):
+      the single-launch merge.  With at most 8 pairs, splits of 32 keys (64
+      with more than 2 pairs), at most 16 -- e.g. config 1 (B=1, L=512): 16
+      splits (5.46 us against 5.58 at 8 and 6.23 for 16 split + combine);
+      B=1, L=2048: 16 (6.23 against 6.47 for 64 split + combine); config 2
+      (B=4, cap 2048, ragged with a bias): 16 (7.00 against 7.31 for 32 split
+      + combine).  With more pairs, splits of 128 keys, at most 192
+      workgroups -- e.g. B=8, L=512: 4 (6.55 against 6.72 for 16 split +
+      combine);
+    * longer rows: split + combine launches with one workgroup per CU
+      (``NUM_CUS // pairs`` splits), at most 128 splits and none shorter than
+      64 keys -- e.g. config 3 (B=1, L=32768): 128 (9.24 us); B=4, L=4096: 32
+      (7.84 against 8.25 for 16 fused splits); B=4, L=16384: 32 (11.79
+      against 12.44 for 128); B=8, L=1536: 16 (7.53 against 8.08 for 12
+      fused); B=5, L=5000: 25 (8.82 against 9.51 for 39).  Write-through
+      partials and non-temporal tile loads made the two launches the faster
+      form here: the combine launch now costs less than the single-launch
+      merge's serial tail.
 
     More pairs: one workgroup per CU (``_fill_splits``), single launch.  (The reference's
     rule, ``max(1, min(32, 272 // (B*KVH), cap // 256))`` at SE:1027, targets
@@ -89,15 +94,14 @@ def decode_plan(batch: int, kv_heads: int, length: int) -> tuple[int, bool]:
     if pairs > 16:
         s = _fill_splits(pairs, length)
         return s, prefer_fused(s)
-    if pairs <= 8 and (length <= 2048 or (length <= 4096 and pairs > 2)):
+    if pairs <= 8 and length <= 2048:
         keys = 32 if pairs <= 2 else 64
         s = max(1, min(math.ceil(length / keys), 16))
         return s, s > 1
-    if length <= 2048 or (length <= 4096 and pairs <= 2):
-        keys = 64 if pairs <= 2 else 128
-        s = max(1, min(math.ceil(length / keys), 192 // pairs, 32))
+    if length <= 512:
+        s = max(1, min(math.ceil(length / 128), 192 // pairs, 32))
         return s, s > 1
-    s = max(1, min(max(length // 128, NUM_CUS // pairs), 128, 4 * NUM_CUS // pairs))
+    s = max(1, min(NUM_CUS // pairs, 128, math.ceil(length / 64)))
     return s, False
 
 

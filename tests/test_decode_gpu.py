@@ -76,11 +76,12 @@ def test_config2_ragged_24_layers(dev, use_kv_last):
 
 
 @pytest.mark.parametrize("batch,length", [(1, 8192), (2, 4096), (4, 8192), (8, 2048), (8, 4096),
-                                          (3, 5000)])
+                                          (3, 5000), (1, 2500), (8, 512)])
 def test_decode_plan_shapes_match_oracle(dev, batch, length):
     """The default plan (ops.decode_plan) at the shapes where it picks split +
-    combine launches with 32-128 splits or a capped single launch; rows
-    ragged through kv_last, stale NaN past each row's last slot."""
+    combine launches with 16-128 splits (one workgroup per CU, or fewer
+    64-key splits) or a capped single launch; rows ragged through kv_last,
+    stale NaN past each row's last slot."""
     case = workloads.decode_uniform(batch, length, seed=length + batch)
     gen = torch.Generator().manual_seed(batch)
     lengths = torch.randint(length // 2, length + 1, (batch,), generator=gen).tolist()

@@ -11,20 +11,24 @@ from qwenforge_amd import ops
 
 
 @pytest.mark.parametrize("batch,length,splits,fused", [
-    (1, 512, 16, True),      # config 1: 32-key splits, single launch (5.99 us vs 6.17 at 8)
-    (1, 2048, 16, True),     # 128-key splits: 6.70 us vs 7.04 at 32
+    (1, 512, 16, True),      # config 1: 32-key splits, single launch (5.46 us vs 5.58 at 8)
+    (1, 2048, 16, True),     # 128-key splits: 6.23 us vs 6.47 for 64 split + combine
     (2, 512, 8, True),       # 6.23 us vs 6.58 at 4
     (4, 512, 8, True),       # 6.55 us vs 6.70 at 4
-    (4, 2048, 16, True),     # config 2 (cap 2048): 128-key splits, single launch
+    (4, 2048, 16, True),     # config 2 (cap 2048): 7.00 us vs 7.31 for 32 split + combine
+    (8, 512, 4, True),       # 16 pairs, short rows: 6.55 us vs 6.72 for 16 split + combine
     (1, 32768, 128, False),  # config 3: split + combine
-    (1, 4096, 32, True),     # <= 2 pairs and <= 4096 keys: single launch
-    (1, 8192, 128, False),   # 8.6 us against 9.3 for 32 fused splits
-    (2, 4096, 16, True),     # 7.82 us vs 8.07 for 64 split + combine
-    (4, 4096, 16, True),     # 8.57 us vs 8.87 for 32 split + combine
-    (4, 8192, 64, False),    # 10.9 us against 12.2
-    (8, 2048, 12, True),     # at most 192 workgroups with the single launch
-    (8, 4096, 32, False),    # 11.0 us against 11.9
-    (8, 16384, 64, False),   # at most 1024 workgroups
+    (1, 4096, 64, False),    # one workgroup per CU, 64-key splits: 6.71 us vs 6.96 at 32 fused
+    (1, 8192, 128, False),   # 7.10 us
+    (2, 4096, 64, False),    # 7.05 us vs 7.45 for 16 fused splits
+    (4, 4096, 32, False),    # 7.84 us vs 8.25 for 16 fused splits
+    (4, 8192, 32, False),    # 9.14 us vs 9.41 at 64
+    (4, 16384, 32, False),   # 11.79 us vs 12.44 at 128
+    (8, 2048, 16, False),    # 7.87 us vs 8.19 for 12 fused splits
+    (8, 4096, 16, False),    # 9.15 us vs 9.39 at 32
+    (8, 16384, 16, False),   # 16.79 us vs 17.71 at 64
+    (5, 5000, 25, False),    # 8.82 us vs 9.51 at 39
+    (1, 2500, 40, False),    # 64-key floor: 40 splits, 80 workgroups
     (16, 32768, 8, True),    # bandwidth regime: one workgroup per CU
     (64, 4096, 2, True),
     (12, 5760, 10, True),    # the reference's benchmark shape: once per CU (12.55 vs 13.35 us at 21)
@@ -51,11 +55,12 @@ def test_workgroup_counts_stay_in_the_measured_ranges(batch):
         if s == 1:
             continue  # at least as many pairs as CUs, or a row too short to split
         if pairs <= 16:
-            # Single launch: at most 192 workgroups; two launches: from a full
-            # fill of the CUs (floor(CUs / pairs) splits, never a count just
-            # above it) to four per CU, or 128 splits.
-            full = ops.NUM_CUS // pairs * pairs
-            assert (wg <= 192) if fused else (full <= wg <= 4 * ops.NUM_CUS or s == 128), \
+            # Single launch: at most 192 workgroups; two launches: one
+            # workgroup per CU (floor(CUs / pairs) splits, never a count just
+            # above it), fewer only where 64-key splits or 128 splits cap it.
+            full = ops.NUM_CUS // pairs
+            want = min(full, 128, -(-length // 64))
+            assert (wg <= 192) if fused else (s == want and wg <= ops.NUM_CUS), \
                 (batch, length, s)
         else:
             # Once per CU.
