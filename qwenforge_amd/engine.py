@@ -18,6 +18,10 @@ Mirrors the reference's cached generation path without the tokenizer:
   argmax.  The per-step bookkeeping the reference does on the host between
   replays (bias slot, write slot, positions, token store; SE:1126-1132) runs
   inside the graph as device ops, so a step is a single graph replay.
+  Captured steps are kept per (batch, capacity, padded) in a ``GraphRegistry``
+  (the reference's LRU registry under a 2.4 GB KV budget, SE:393-394 and
+  SE:1090-1118): a later call of the same shape prefills into that entry's
+  caches and only replays.
 
 For batches of 1..4 rows the decode step body is the fused weight-streaming
 path (``step_ops``, include/qf_step.h): per layer one launch for rms_norm +
@@ -30,6 +34,8 @@ projections.  Everything is fp16 storage with the reference's rounding points.
 """
 
 from __future__ import annotations
+
+from collections import OrderedDict
 
 import torch
 import torch.nn.functional as F
@@ -48,6 +54,54 @@ def cache_capacity(prompt_len: int, new_tokens: int, multiple: int = 64) -> int:
     return (cap + multiple - 1) // multiple * multiple
 
 
+class GraphRegistry:
+    """Captured decode-step contexts, least recently used first.
+
+    The reference keys them by (batch, capacity) and, after each capture,
+    evicts the oldest entries while the persistent KV caches of all entries
+    exceed a byte budget, never the entry just stored (SE:1090-1103, budget
+    2.4 GB at SE:394); a hit moves the entry to the newest end (SE:1115-1118).
+    """
+
+    def __init__(self, byte_budget: int = 2_400_000_000):
+        self.byte_budget = byte_budget
+        self._entries: OrderedDict = OrderedDict()
+
+    @staticmethod
+    def kv_bytes(ctx) -> int:
+        """Bytes of a context's per-layer K and V caches (SE:1094-1096)."""
+        return sum(k.numel() * k.element_size() + v.numel() * v.element_size()
+                   for k, v in ctx["caches"])
+
+    def get(self, key):
+        """The context stored under ``key`` (now the most recently used), or None."""
+        ctx = self._entries.pop(key, None)
+        if ctx is not None:
+            self._entries[key] = ctx
+        return ctx
+
+    def put(self, key, ctx) -> None:
+        """Store ``ctx`` as the most recently used entry, then evict the least
+        recently used ones while the budget is exceeded."""
+        self._entries.pop(key, None)
+        self._entries[key] = ctx
+        total = sum(self.kv_bytes(c) for c in self._entries.values())
+        while total > self.byte_budget and len(self._entries) > 1:
+            oldest = next(iter(self._entries))
+            if oldest == key:
+                break
+            total -= self.kv_bytes(self._entries.pop(oldest))
+
+    def clear(self) -> None:
+        self._entries.clear()
+
+    def keys(self) -> list:
+        return list(self._entries)
+
+    def __len__(self) -> int:
+        return len(self._entries)
+
+
 class DecodeEngine:
     """Batched greedy decoding of a Qwen2-shaped model on one MI355X."""
 
@@ -62,6 +116,8 @@ class DecodeEngine:
         self.tile_weights = tile_weights
         self._tiles = None
         self._ctx = None
+        self.graphs = GraphRegistry()
+        self.captures = 0  # graph captures so far (registry hits capture nothing)
 
     # Rows from which the fused step reads the QKV and gate/up weights as
     # matrix-core tiles (batch rows as MFMA columns): measured on MI355X at
@@ -322,7 +378,32 @@ class DecodeEngine:
             ctx["bias"][:, cap - 1] = torch.finfo(torch.float16).min
         torch.cuda.synchronize(self.device)
         ctx["graph"] = graph
+        self.captures += 1
         return graph
+
+    def _graph_context(self, key, batch: int, cap: int, prefill, bias_mask=None):
+        """Run ``prefill(caches)`` into the registry entry ``key`` = (batch,
+        cap, padded) and return (context, what prefill returned), capturing
+        the step on a miss.
+
+        On a hit the prompt overwrites the entry's cache rows and the bias is
+        rebuilt from ``bias_mask``; slots a previous call wrote past the new
+        prompt are either masked by the bias (holes) or beyond the write slot,
+        which bounds every attention read, and each decode step writes its
+        slot before attending it (SE:1104-1114).  The rows buffer holds
+        ``cap`` columns, the most new tokens a call of this capacity asks for.
+        """
+        ctx = self.graphs.get(key)
+        caches = ctx["caches"] if ctx is not None else self.new_caches(batch, cap)
+        result = prefill(caches)
+        if ctx is None:
+            ctx = self.make_context(caches, batch, cap, bias_mask=bias_mask)
+            self.capture(ctx)
+            self.graphs.put(key, ctx)
+        elif bias_mask is not None:
+            ctx["bias"].fill_(torch.finfo(torch.float16).min)
+            ctx["bias"].masked_fill_(bias_mask, 0.0)
+        return ctx, result
 
     @torch.no_grad()
     def generate_ragged(self, prompts, max_new_tokens: int, timing: dict | None = None):
@@ -331,23 +412,25 @@ class DecodeEngine:
         The reference's padded-batch semantics (SE:1241-1335): capacity =
         roundup64(max_len + new - 1); row b's prompt fills slots [0, len_b);
         decode step t writes the shared slot max_len + t - 1 at position
-        len_b + t - 1, and the bias masks the holes [len_b, max_len).
+        len_b + t - 1, and the bias masks the holes [len_b, max_len).  Captured
+        steps are reused per (batch, capacity) as in ``generate``.
         """
         b = len(prompts)
         lengths = [int(p.numel()) for p in prompts]
         p_max = max(lengths)
         cap = cache_capacity(p_max, max_new_tokens)
-        caches = self.new_caches(b, cap)
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
-        ev[0].record()
-        logits = self.prefill_ragged(prompts, caches)
-        first = torch.argmax(logits, dim=-1)
-        ev[1].record()
         mask = torch.zeros(b, cap, dtype=torch.bool, device=self.device)
         for i, n in enumerate(lengths):
             mask[i, :n] = True
-        ctx = self.make_context(caches, b, max_new_tokens, bias_mask=mask)
-        self.capture(ctx)
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        ev[0].record()
+
+        def run_prefill(caches):
+            first = torch.argmax(self.prefill_ragged(prompts, caches), dim=-1)
+            ev[1].record()
+            return first
+
+        ctx, first = self._graph_context((b, cap, True), b, cap, run_prefill, bias_mask=mask)
         ctx["rows"][:, 0] = first
         ctx["token"].copy_(first)
         ctx["pos"].copy_(torch.tensor(lengths, device=self.device))
@@ -363,26 +446,29 @@ class DecodeEngine:
             timing["prefill_ms"] = ev[0].elapsed_time(ev[1])
             timing["decode_ms"] = ev[2].elapsed_time(ev[3])
         self._ctx = ctx
-        return ctx["rows"].clone()
+        return ctx["rows"][:, :max_new_tokens].clone()
 
     @torch.no_grad()
     def generate(self, input_ids: torch.Tensor, max_new_tokens: int, timing: dict | None = None):
         """Greedy ids (B, max_new_tokens) for equal-length prompts (B, S).
 
         Capacity follows SE:1263-1273: prompt + new - 1, rounded up to 64.
-        ``timing`` (optional dict) receives prefill and decode times in ms
-        (HIP events on the current stream).
+        A call whose (batch, capacity) is in ``graphs`` reuses that captured
+        step and its caches.  ``timing`` (optional dict) receives prefill and
+        decode times in ms (HIP events on the current stream; a capture falls
+        between the two and is in neither).
         """
         b, s = input_ids.shape
         cap = cache_capacity(s, max_new_tokens)
-        caches = self.new_caches(b, cap)
         ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
         ev[0].record()
-        logits = self.prefill(input_ids, caches)
-        first = torch.argmax(logits, dim=-1)
-        ev[1].record()
-        ctx = self.make_context(caches, b, max_new_tokens)
-        self.capture(ctx)
+
+        def run_prefill(caches):
+            first = torch.argmax(self.prefill(input_ids, caches), dim=-1)
+            ev[1].record()
+            return first
+
+        ctx, first = self._graph_context((b, cap, False), b, cap, run_prefill)
         ctx["rows"][:, 0] = first
         ctx["token"].copy_(first)
         ctx["pos"].fill_(s)
@@ -398,4 +484,4 @@ class DecodeEngine:
             timing["prefill_ms"] = ev[0].elapsed_time(ev[1])
             timing["decode_ms"] = ev[2].elapsed_time(ev[3])
         self._ctx = ctx
-        return ctx["rows"].clone()
+        return ctx["rows"][:, :max_new_tokens].clone()

@@ -132,7 +132,7 @@ def test_generate_full_shape_128_tokens(dev, batch):
     assert ctx["caches"][0][0].shape[2] == oracle.capacity(1024, 128) == 1152
     assert int(ctx["write"].item()) == 1151 and int(ctx["step"].item()) == 128
     assert ctx["pos"].cpu().tolist() == [1151] * batch
-    assert torch.equal(rows[:, 1:], ctx["rows"][:, 1:])
+    assert torch.equal(rows[:, 1:], ctx["rows"][:, 1:128])
 
 
 def test_generate_ragged_full_shape_bookkeeping(dev):
@@ -291,3 +291,50 @@ def test_generate_ragged_runs(dev):
     rows = eng.generate_ragged(prompts, 12)
     assert rows.shape == (3, 12)
     assert int(rows.min()) >= 0 and int(rows.max()) < cfg.vocab
+
+
+def test_generate_reuses_the_captured_step(dev):
+    """A second call of the same (batch, capacity) prefills into the stored
+    caches and replays the stored graph (no capture; SE:1104-1118), and its
+    tokens equal a fresh engine's for the same prompts, although the stored
+    caches hold the first call's rows past the new prompt.  Another capacity
+    is a second entry; coming back to the first one captures nothing."""
+    cfg = Qwen2Config(layers=2)
+    w = init_weights(cfg, dev, seed=4)
+    eng = DecodeEngine(cfg, w, dev)
+    gen = torch.Generator().manual_seed(11)
+    a1 = torch.randint(0, cfg.vocab, (2, 200), generator=gen).to(dev)
+    a2 = torch.randint(0, cfg.vocab, (2, 190), generator=gen).to(dev)   # same capacity, 256
+    c1 = torch.randint(0, cfg.vocab, (2, 300), generator=gen).to(dev)   # capacity 320
+    eng.generate(a1, 40)
+    assert eng.captures == 1 and eng.graphs.keys() == [(2, 256, False)]
+    got = eng.generate(a2, 24)
+    assert eng.captures == 1
+    want = DecodeEngine(cfg, w, dev).generate(a2, 24)
+    assert torch.equal(got, want)
+    eng.generate(c1, 12)
+    assert eng.captures == 2 and eng.graphs.keys() == [(2, 256, False), (2, 320, False)]
+    got = eng.generate(a1, 40)
+    assert eng.captures == 2 and eng.graphs.keys() == [(2, 320, False), (2, 256, False)]
+    assert torch.equal(got, DecodeEngine(cfg, w, dev).generate(a1, 40))
+
+
+@pytest.mark.parametrize("batch", [3, 6])
+def test_generate_ragged_reuses_the_captured_step(dev, batch):
+    """Padded batches through the registry: the second call has other
+    lengths (other holes) in the same capacity, so the stored bias is
+    rebuilt from the new mask; tokens equal a fresh engine's.  Batch 6 runs
+    the torch-projection step, batch 3 the fused one."""
+    cfg = Qwen2Config(layers=2)
+    w = init_weights(cfg, dev, seed=5)
+    eng = DecodeEngine(cfg, w, dev)
+    gen = torch.Generator().manual_seed(batch)
+    first = [torch.randint(0, cfg.vocab, (n,), generator=gen).to(dev)
+             for n in (60, 250, 130, 201, 17, 90)[:batch]]
+    second = [torch.randint(0, cfg.vocab, (n,), generator=gen).to(dev)
+              for n in (240, 33, 199, 120, 250, 5)[:batch]]
+    eng.generate_ragged(first, 6)
+    got = eng.generate_ragged(second, 6)
+    assert eng.captures == 1 and eng.graphs.keys() == [(batch, 256, True)]
+    assert torch.equal(got, DecodeEngine(cfg, w, dev).generate_ragged(second, 6))
+
