@@ -381,10 +381,16 @@ class DecodeEngine:
         self.captures += 1
         return graph
 
-    def _graph_context(self, key, batch: int, cap: int, prefill, bias_mask=None):
+    # Fewest new tokens for which generate captures the step (SE:1274-1276):
+    # shorter runs call the step eagerly, and a single token decodes nothing.
+    GRAPH_MIN_NEW_TOKENS = 8
+
+    def _graph_context(self, key, batch: int, cap: int, prefill, bias_mask=None,
+                       capture: bool = True):
         """Run ``prefill(caches)`` into the registry entry ``key`` = (batch,
         cap, padded) and return (context, what prefill returned), capturing
-        the step on a miss.
+        the step on a miss -- or, with ``capture`` False and no entry, into a
+        fresh context that is neither captured nor stored.
 
         On a hit the prompt overwrites the entry's cache rows and the bias is
         rebuilt from ``bias_mask``; slots a previous call wrote past the new
@@ -398,12 +404,19 @@ class DecodeEngine:
         result = prefill(caches)
         if ctx is None:
             ctx = self.make_context(caches, batch, cap, bias_mask=bias_mask)
-            self.capture(ctx)
-            self.graphs.put(key, ctx)
+            if capture:
+                self.capture(ctx)
+                self.graphs.put(key, ctx)
         elif bias_mask is not None:
             ctx["bias"].fill_(torch.finfo(torch.float16).min)
             ctx["bias"].masked_fill_(bias_mask, 0.0)
         return ctx, result
+
+    def _replay_fn(self, ctx):
+        """One decode step of ``ctx``: its graph's replay, or the step called
+        eagerly when it was not captured (same results bit for bit)."""
+        graph = ctx.get("graph")
+        return graph.replay if graph is not None else (lambda: self._step(ctx))
 
     @torch.no_grad()
     def generate_ragged(self, prompts, max_new_tokens: int, timing: dict | None = None):
@@ -430,7 +443,8 @@ class DecodeEngine:
             ev[1].record()
             return first
 
-        ctx, first = self._graph_context((b, cap, True), b, cap, run_prefill, bias_mask=mask)
+        ctx, first = self._graph_context((b, cap, True), b, cap, run_prefill, bias_mask=mask,
+                                         capture=max_new_tokens >= self.GRAPH_MIN_NEW_TOKENS)
         ctx["rows"][:, 0] = first
         ctx["token"].copy_(first)
         ctx["pos"].copy_(torch.tensor(lengths, device=self.device))
@@ -438,8 +452,9 @@ class DecodeEngine:
         ctx["step"].fill_(1)
         torch.cuda.synchronize(self.device)
         ev[2].record()
+        step = self._replay_fn(ctx)
         for _ in range(1, max_new_tokens):
-            ctx["graph"].replay()
+            step()
         ev[3].record()
         torch.cuda.synchronize(self.device)
         if timing is not None:
@@ -454,7 +469,8 @@ class DecodeEngine:
 
         Capacity follows SE:1263-1273: prompt + new - 1, rounded up to 64.
         A call whose (batch, capacity) is in ``graphs`` reuses that captured
-        step and its caches.  ``timing`` (optional dict) receives prefill and
+        step and its caches; below GRAPH_MIN_NEW_TOKENS new tokens a call that
+        finds none runs the step eagerly instead of capturing it.  ``timing`` (optional dict) receives prefill and
         decode times in ms (HIP events on the current stream; a capture falls
         between the two and is in neither).
         """
@@ -468,7 +484,8 @@ class DecodeEngine:
             ev[1].record()
             return first
 
-        ctx, first = self._graph_context((b, cap, False), b, cap, run_prefill)
+        ctx, first = self._graph_context((b, cap, False), b, cap, run_prefill,
+                                         capture=max_new_tokens >= self.GRAPH_MIN_NEW_TOKENS)
         ctx["rows"][:, 0] = first
         ctx["token"].copy_(first)
         ctx["pos"].fill_(s)
@@ -476,8 +493,9 @@ class DecodeEngine:
         ctx["step"].fill_(1)
         torch.cuda.synchronize(self.device)
         ev[2].record()
+        step = self._replay_fn(ctx)
         for _ in range(1, max_new_tokens):
-            ctx["graph"].replay()
+            step()
         ev[3].record()
         torch.cuda.synchronize(self.device)
         if timing is not None:

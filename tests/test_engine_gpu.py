@@ -332,9 +332,24 @@ def test_generate_ragged_reuses_the_captured_step(dev, batch):
     first = [torch.randint(0, cfg.vocab, (n,), generator=gen).to(dev)
              for n in (60, 250, 130, 201, 17, 90)[:batch]]
     second = [torch.randint(0, cfg.vocab, (n,), generator=gen).to(dev)
-              for n in (240, 33, 199, 120, 250, 5)[:batch]]
-    eng.generate_ragged(first, 6)
-    got = eng.generate_ragged(second, 6)
-    assert eng.captures == 1 and eng.graphs.keys() == [(batch, 256, True)]
-    assert torch.equal(got, DecodeEngine(cfg, w, dev).generate_ragged(second, 6))
+              for n in (260, 33, 199, 120, 250, 5)[:batch]]
+    eng.generate_ragged(first, 8)
+    got = eng.generate_ragged(second, 8)
+    assert eng.captures == 1 and eng.graphs.keys() == [(batch, 320, True)]
+    assert torch.equal(got, DecodeEngine(cfg, w, dev).generate_ragged(second, 8))
 
+
+
+def test_short_generations_run_the_step_eagerly(dev):
+    """Below 8 new tokens nothing is captured or stored (SE:1274-1276): the
+    step runs eagerly, and one token is the prefill's argmax alone.  The
+    tokens are those of a captured run."""
+    cfg = Qwen2Config(layers=2)
+    w = init_weights(cfg, dev, seed=6)
+    ids = torch.randint(0, cfg.vocab, (2, 200), generator=torch.Generator().manual_seed(3)).to(dev)
+    eng = DecodeEngine(cfg, w, dev)
+    short = eng.generate(ids, 4)
+    one = eng.generate(ids, 1)
+    assert eng.captures == 0 and len(eng.graphs) == 0
+    full = DecodeEngine(cfg, w, dev).generate(ids, 8)
+    assert torch.equal(short, full[:, :4]) and torch.equal(one, full[:, :1])
