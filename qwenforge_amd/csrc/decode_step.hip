@@ -18,6 +18,10 @@
 //     bias + RoPE + KV append (QKV), SwiGLU (gate/up), residual add (o_proj,
 //     down), and a per-block argmax key (lm_head).
 //
+// The down projection departs from this shape: its rows are long (K = 4864),
+// so each row is split between the two waves of its own workgroup, and each
+// lane loads the activation chunks it needs straight into registers.
+//
 // Replaces the torch op sequence of _decode_step_static
 // (student_engine.py:896-982); see include/qf_step.h for the per-entry-point
 // mapping and rounding.
@@ -397,6 +401,70 @@ __global__ __launch_bounds__(kNT) void gemv_residual_kernel(GemvArgs a) {
     for (int bb = 0; bb < NB; ++bb)
       if (r == rr && b == bb) v = acc[rr][bb];
   if (n0 + r >= a.N) return;
+  *hp = (f16)(resid + (float)(f16)v);
+}
+
+// Long rows (down_proj): RPW rows per workgroup, each split between KP waves
+// (contiguous parts of ceil(C / KP) chunks, whose sums meet in LDS and are
+// added in part order).  Nothing is staged: each lane loads the activation
+// chunks it multiplies straight into registers (L2 hits, issued right after
+// its weight loads), so no barrier stands between the loads and the dot
+// products.  Measured on MI355X at K = 4864, N = 896, weights past the MALL,
+// against one row per wave of a four-wave workgroup with the activation
+// staged through LDS: KP = 2, RPW = 1 takes B=1 3.81-3.86 vs 4.35 us, B=2
+// 4.32 vs 4.81, B=4 5.02-5.11 vs 5.42 (RPW = 4 with the activation staged:
+// 4.03-4.09 / 4.45-4.51 / 5.46-5.51).  Rounding: fp16(residual + fp16(acc)).
+template <int NB, int NS, int KP, int RPW>
+__global__ __launch_bounds__(KP * RPW * 64) void gemv_residual_direct_kernel(GemvArgs a) {
+  __shared__ float red[KP][RPW][NB];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int rw = w % RPW, part = w / RPW;
+  const int K = a.K, C = K / 8, Cp = (C + KP - 1) / KP;
+  const int c0 = part * Cp, c1 = min(c0 + Cp, C);
+  const int n0 = blockIdx.x * RPW + rw;
+  const int nr = min(n0, a.N - 1);
+  const int be = lane < NB ? lane : 0;
+  f16* hp = a.hidden + be * a.h_sb + nr;
+  const float resid = (float)*hp;
+  const f16* wrow = a.w + (int64_t)nr * K;
+  f16x8 wr[NS], xr[NB][NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) wr[s] = load16_nt(wrow + 8 * min(c0 + 64 * s + lane, c1 - 1));
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const int c = min(c0 + 64 * s + lane, c1 - 1);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) xr[b][s] = load16(a.inp + b * a.in_sb + 8 * c);
+  }
+  float acc[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) acc[b] = 0.f;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const bool in = c0 + 64 * s + lane < c1;
+    const f16x8 wv = in ? wr[s] : zero8();
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[b] = dot8(wv, xr[b][s], acc[b]);
+  }
+#pragma unroll
+  for (int b = 0; b < NB; ++b) acc[b] = wave_sum(acc[b]);
+  if (KP > 1) {
+    if (lane == 0) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b) red[part][rw][b] = acc[b];
+    }
+    __syncthreads();
+  }
+  if (part != 0 || n0 >= a.N || lane >= NB) return;
+  float v = 0.f;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    if (lane == b) {
+      v = acc[b];
+#pragma unroll
+      for (int p = 1; p < KP; ++p) v += red[p][rw][b];
+    }
+  }
   *hp = (f16)(resid + (float)(f16)v);
 }
 
@@ -1190,25 +1258,16 @@ extern "C" int qf_gemv_residual(const void* inp, int64_t in_sb, const void* w, v
     if (B * C <= kNT) { QF_DISPATCH_B(B, gemv_residual_kernel, 2, 2, 1) }
     else { QF_DISPATCH_B(B, gemv_residual_kernel, 2, 2, 2) }
   } else {
-    // Long rows (down_proj): one row per wave, the whole row in flight, with
-    // as many 64-lane chunk rounds as the row needs (10 for K = 4864).
-    const dim3 grid((N + kNW - 1) / kNW);
-    const int ns = (C + 63) / 64;
-    // XP: 16-byte input chunks staged per thread (B * C <= XP * kNT).
-    if (ns <= 10) {
-      if (B * C <= 4 * kNT) { QF_DISPATCH_B(B, gemv_residual_kernel, 10, 1, 4) }
-      else if (B * C <= 8 * kNT) { QF_DISPATCH_B(B, gemv_residual_kernel, 10, 1, 8) }
-      else if (B * C <= 10 * kNT) { QF_DISPATCH_B(B, gemv_residual_kernel, 10, 1, 10) }
-      else { QF_DISPATCH_B(B, gemv_residual_kernel, 10, 1, 16) }
-    } else if (ns <= 12) {
-      if (B * C <= 4 * kNT) { QF_DISPATCH_B(B, gemv_residual_kernel, 12, 1, 4) }
-      else if (B * C <= 8 * kNT) { QF_DISPATCH_B(B, gemv_residual_kernel, 12, 1, 8) }
-      else { QF_DISPATCH_B(B, gemv_residual_kernel, 12, 1, 16) }
-    } else {
-      if (B * C <= 4 * kNT) { QF_DISPATCH_B(B, gemv_residual_kernel, 16, 1, 4) }
-      else if (B * C <= 8 * kNT) { QF_DISPATCH_B(B, gemv_residual_kernel, 16, 1, 8) }
-      else { QF_DISPATCH_B(B, gemv_residual_kernel, 16, 1, 16) }
-    }
+    // Long rows (down_proj): gemv_residual_direct_kernel, one row per
+    // workgroup split between two waves, nothing staged in LDS; 5 chunk
+    // rounds per wave up to K = 5120 (K = 4864: 4.75), 8 up to kMaxK.
+    constexpr int kKP = 2, kRPW = 1;
+    const dim3 gridd((N + kRPW - 1) / kRPW), blockd(kKP * kRPW * 64);
+    const dim3& grid = gridd;
+    const dim3& block = blockd;
+    const size_t shm = 0;
+    if ((C + kKP - 1) / kKP <= 5 * 64) { QF_DISPATCH_B(B, gemv_residual_direct_kernel, 5, kKP, kRPW) }
+    else { QF_DISPATCH_B(B, gemv_residual_direct_kernel, 8, kKP, kRPW) }
   }
   return (int)hipGetLastError();
 }
