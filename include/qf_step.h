@@ -122,9 +122,12 @@ int qf_rms_gate_up_swiglu(const void* x, int64_t x_sb, const void* norm_w, float
  * n_blocks, keys[b * n_blocks + j] = the block's best (logit, index) packed
  * so that the largest key is the largest logit with the smallest index
  * (torch.argmax's first-maximum rule).  keys: B * n_blocks uint64 (device).
- * Supports hidden <= 1024, B in 1..4, 1 <= n_blocks <= 65535. */
+ * w_lm: (V, hidden) as rows (w_layout QF_W_ROWS) or packed with
+ * QF_PACK_PLAIN (QF_W_TILES: V % 16 == 0, hidden % 32 == 0, logits 8-byte
+ * aligned with lg_sb % 4 == 0).  Supports hidden <= 1024, B in 1..4,
+ * 1 <= n_blocks <= 65535. */
 int qf_rms_lm_head(const void* x, int64_t x_sb, const void* norm_w, float eps,
-                   const void* w_lm, void* logits, int64_t lg_sb, uint64_t* keys,
+                   const void* w_lm, int w_layout, void* logits, int64_t lg_sb, uint64_t* keys,
                    int n_blocks, int B, int hidden, int V, void* stream);
 
 /* Reduces the per-block keys of qf_rms_lm_head to the argmax token and does

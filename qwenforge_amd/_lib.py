@@ -130,7 +130,7 @@ SIGNATURES = {
     ],
     "qf_rms_lm_head": [
         _vp, _i64, _vp, _f32,           # x, x_sb, norm_w, eps
-        _vp, _vp, _i64, _vp,            # w_lm, logits, lg_sb, keys
+        _vp, _i32, _vp, _i64, _vp,      # w_lm, w_layout, logits, lg_sb, keys
         _i32, _i32, _i32, _i32,         # n_blocks, B, hidden, V
         _vp,                            # stream
     ],

@@ -130,7 +130,7 @@ class PagedDecodeEngine(DecodeEngine):
             step_ops.attn_merge_o_proj(ctx["flash"], layer["o_weight"], hidden)
             step_ops.rms_gate_up_swiglu(hidden, layer["post_norm"], eps, w_gate_up, h)
             step_ops.gemv_residual(h, layer["down_weight"], hidden)
-        step_ops.rms_lm_head(hidden, self.w["final_norm"], eps, self.w["lm_head"], ctx["logits"],
+        step_ops.rms_lm_head(hidden, self.w["final_norm"], eps, self.lm_head_weight(b), ctx["logits"],
                              ctx["keys"])
         step_ops.argmax_step(ctx["keys"], ctx["token"], ctx["rows"], ctx["step"], None, pos)
 

@@ -247,22 +247,23 @@ def rms_gate_up_swiglu(x: torch.Tensor, norm_w: torch.Tensor, eps: float, w_gate
     _lib.check(rc, "qf_rms_gate_up_swiglu")
 
 
-def rms_lm_head(x: torch.Tensor, norm_w: torch.Tensor, eps: float, w_lm: torch.Tensor,
+def rms_lm_head(x: torch.Tensor, norm_w: torch.Tensor, eps: float, w_lm,
                 logits: torch.Tensor, keys: torch.Tensor) -> None:
     """logits <- fp16(rms_norm(x) @ w_lm^T); keys (B, n_blocks) uint64-as-int64
-    <- per-block argmax keys."""
+    <- per-block argmax keys.  ``w_lm``: the (V, hidden) weight, or its
+    ``Tiles`` packed with PACK_PLAIN (matrix-core kernel)."""
     b, hidden = x.shape
     _batch(b)
     vocab = w_lm.shape[0]
     x_sb = _rows("x", x, b, hidden)
     _check("norm_w", norm_w)
-    _weight("w_lm", w_lm, vocab, hidden)
+    w_ptr, w_layout = _weight("w_lm", w_lm, vocab, hidden, PACK_PLAIN)
     lg_sb = _rows("logits", logits, b, vocab)
     _check("keys", keys, torch.int64)
     if keys.dim() != 2 or keys.shape[0] != b or not keys.is_contiguous():
         raise ValueError("keys must be contiguous (B, n_blocks) int64")
     rc = _lib.load().qf_rms_lm_head(x.data_ptr(), x_sb, norm_w.data_ptr(), float(eps),
-                                    w_lm.data_ptr(), logits.data_ptr(), lg_sb, keys.data_ptr(),
+                                    w_ptr, w_layout, logits.data_ptr(), lg_sb, keys.data_ptr(),
                                     keys.shape[1], b, hidden, vocab, _stream(x.device))
     _lib.check(rc, "qf_rms_lm_head")
 

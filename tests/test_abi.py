@@ -157,8 +157,12 @@ def test_step_kernels_reject_bad_arguments():
     # tiles need hidden % 32 == 0 and I % 8 == 0
     assert lib.qf_rms_gate_up_swiglu(16, 888, 16, 1e-6, 16, 1, 16, 4864, 1, 888, 4864, None) == -2
     assert lib.qf_rms_gate_up_swiglu(16, 896, 16, 1e-6, 16, 1, 16, 4860, 1, 896, 4860, None) == -2
-    assert lib.qf_rms_lm_head(16, 896, 16, 1e-6, 16, 16, 100, 16, 0, 1, 896, 100, None) == -1
-    assert lib.qf_rms_lm_head(16, 896, 16, 1e-6, 16, 16, 100, 16, 8, 0, 896, 100, None) == -2
+    assert lib.qf_rms_lm_head(16, 896, 16, 1e-6, 16, 0, 16, 100, 16, 0, 1, 896, 100, None) == -1
+    assert lib.qf_rms_lm_head(16, 896, 16, 1e-6, 16, 0, 16, 100, 16, 8, 0, 896, 100, None) == -2
+    assert lib.qf_rms_lm_head(16, 896, 16, 1e-6, 16, 3, 16, 100, 16, 8, 1, 896, 100, None) == -1
+    # tiles need whole 16-row blocks and 8-byte logit stores
+    assert lib.qf_rms_lm_head(16, 896, 16, 1e-6, 16, 1, 16, 104, 16, 8, 2, 896, 100, None) == -2
+    assert lib.qf_rms_lm_head(16, 896, 16, 1e-6, 16, 1, 18, 112, 16, 8, 2, 896, 112, None) == -1
     assert lib.qf_argmax_step(16, 8, 1, 16, 16, 4, 4, None, None, None, None) == -1  # rows w/o step
     assert lib.qf_argmax_step(16, 8, 9, 16, None, 0, 0, None, None, None, None) == -2
     def qkv(cos=16, sin=16, pos=None, inv=None, kc=16, D=64, lay=0):

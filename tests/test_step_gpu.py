@@ -168,10 +168,13 @@ def test_rms_gate_up_swiglu(dev, batch, integer, tiles):
         assert (h.cpu() == ref).float().mean().item() > 0.99
 
 
-@pytest.mark.parametrize("batch", [1, 3, 4])
-def test_rms_lm_head_and_argmax_step(dev, batch):
+@pytest.mark.parametrize("batch,tiles", [(1, False), (3, False), (4, False), (1, True),
+                                         (2, True), (3, True), (4, True)])
+def test_rms_lm_head_and_argmax_step(dev, batch, tiles):
+    """Exact integer logits and the first-maximum argmax on a planted tie, for
+    the row kernel and the matrix-core kernel (packed weight)."""
     gen = torch.Generator().manual_seed(30 + batch)
-    vocab = 5003  # not a multiple of the 4-row groups
+    vocab = 5008 if tiles else 5003  # tiles: whole 16-row blocks; rows: not 4-row groups
     x = _int_rows(batch, HIDDEN, gen)
     nw = torch.ones(HIDDEN, dtype=torch.float16)
     w = _int_w(vocab, HIDDEN, gen)
@@ -180,8 +183,11 @@ def test_rms_lm_head_and_argmax_step(dev, batch):
     w[4000] = w[1234]
     logits = torch.zeros(batch, vocab, device=dev, dtype=torch.float16)
     keys = torch.zeros(batch, 96, device=dev, dtype=torch.long)
-    print(f"[lm_head] B={batch}", flush=True)
-    step_ops.rms_lm_head(x.to(dev), nw.to(dev), EPS, w.to(dev), logits, keys)
+    print(f"[lm_head] B={batch} tiles={tiles}", flush=True)
+    wd = w.to(dev)
+    if tiles:
+        wd = step_ops.pack_weight(wd, step_ops.PACK_PLAIN)
+    step_ops.rms_lm_head(x.to(dev), nw.to(dev), EPS, wd, logits, keys)
     token = torch.full((batch,), -1, device=dev, dtype=torch.long)
     rows = torch.zeros(batch, 5, device=dev, dtype=torch.long)
     step = torch.tensor([2], device=dev)
@@ -199,15 +205,19 @@ def test_rms_lm_head_and_argmax_step(dev, batch):
     assert torch.equal(pos.cpu(), torch.arange(batch) + 11)
 
 
-def test_lm_head_random_logits_close(dev):
+@pytest.mark.parametrize("batch,tiles", [(2, False), (2, True), (4, True)])
+def test_lm_head_random_logits_close(dev, batch, tiles):
     gen = torch.Generator().manual_seed(7)
-    batch, vocab = 2, 151936
+    vocab = 151936
     x = _rand(batch, HIDDEN, gen=gen)
     nw = torch.ones(HIDDEN, dtype=torch.float16)
     w = _rand(vocab, HIDDEN, gen=gen, std=0.02)
     logits = torch.zeros(batch, vocab, device=dev, dtype=torch.float16)
     keys = torch.zeros(batch, step_ops.LM_BLOCKS, device=dev, dtype=torch.long)
-    step_ops.rms_lm_head(x.to(dev), nw.to(dev), EPS, w.to(dev), logits, keys)
+    wd = w.to(dev)
+    if tiles:
+        wd = step_ops.pack_weight(wd, step_ops.PACK_PLAIN)
+    step_ops.rms_lm_head(x.to(dev), nw.to(dev), EPS, wd, logits, keys)
     token = torch.zeros(batch, device=dev, dtype=torch.long)
     step_ops.argmax_step(keys, token)
     torch.cuda.synchronize()
