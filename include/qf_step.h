@@ -97,11 +97,13 @@ int qf_gemv_residual(const void* inp, int64_t in_sb, const void* w,
  * qf_decode_split for all B x KVH x G query heads, rounds the merged rows to
  * fp16 as the combine does (fp16(A * (1/L))) and applies the projection.
  * acc: (B, KVH, splits, G, 64) fp32, m/l: (B, KVH, splits, G) fp32 (m in
- * natural-log units), all contiguous; w_o: (N, KVH*G*64); hidden: (B, N) row
- * stride h_sb, updated in place.  Supports KVH*G*64 <= 1024, B in 1..4. */
+ * natural-log units), all contiguous; w_o: (N, KVH*G*64) as rows (w_layout
+ * QF_W_ROWS) or packed with QF_PACK_PLAIN (QF_W_TILES: N % 16 == 0, hidden
+ * 8-byte aligned with h_sb % 4 == 0); hidden: (B, N) row stride h_sb,
+ * updated in place.  Supports KVH*G*64 <= 1024, B in 1..4. */
 int qf_attn_merge_o_proj(const float* acc, const float* m, const float* l, int splits,
-                         int KVH, int G, const void* w_o, void* hidden, int64_t h_sb,
-                         int B, int N, void* stream);
+                         int KVH, int G, const void* w_o, int w_layout, void* hidden,
+                         int64_t h_sb, int B, int N, void* stream);
 
 /* RMSNorm + gate/up projection + SwiGLU.  Replaces `normalized =
  * rms_norm(hidden, post_norm)` (:976-977) and the first two lines of _mlp

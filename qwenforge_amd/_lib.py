@@ -118,7 +118,7 @@ SIGNATURES = {
     "qf_attn_merge_o_proj": [
         _vp, _vp, _vp, _i32,            # acc, m, l, splits
         _i32, _i32,                     # KVH, G
-        _vp, _vp, _i64,                 # w_o, hidden, h_sb
+        _vp, _i32, _vp, _i64,           # w_o, w_layout, hidden, h_sb
         _i32, _i32,                     # B, N
         _vp,                            # stream
     ],

@@ -487,18 +487,18 @@ struct MergeArgs {
   int K, N;
 };
 
-template <int NB, int RW>
-__global__ __launch_bounds__(kNT) void attn_merge_gemv_residual_kernel(MergeArgs a) {
-  constexpr int NS = kMaxNormK / 8 / 64;
+// The merge prologue shared by the o_proj kernels: every workgroup folds
+// all B x KVH x G x 64 merged attention values into LDS xs (fp16, the
+// combine's rounding).  `issue` runs right after the first batch of partial
+// loads goes out and issues the caller's weight (and residual) loads, so the
+// L2-resident partials land first and the merge runs while the weights are in
+// flight.  Ends with a workgroup barrier.
+template <int NB, typename Issue>
+__device__ __forceinline__ void merge_partials(const MergeArgs& a, f16* xs, Issue&& issue) {
   // Splits folded per batch: the engine's split counts (8 at one row, 4 at
   // more) in one batch, so the merge is one round trip.
   constexpr int kSB = NB == 1 ? 8 : 4;
-  __shared__ __attribute__((aligned(16))) f16 xs[NB * kMaxNormK];
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int K = a.K, C = K / 8;
-  const int n0 = (blockIdx.x * kNW + w) * RW;
-
-  // Merge: item = (b, h, g, 4 dims); xs offset of item `it` is 4 * it because
+  // Item = (b, h, g, 4 dims); xs offset of item `it` is 4 * it because
   // hidden index (h * G + g) * 64 + d matches the (B, KVH, G, D) output layout.
   // Thread t owns items t + kNT*i (i < NB covers NB * KVH * G * 16 <= NB * kNT
   // items); each batch loads kSB splits of every owned item at once.
@@ -557,12 +557,7 @@ __global__ __launch_bounds__(kNT) void attn_merge_gemv_residual_kernel(MergeArgs
   // in flight (a wait for loads issued after the weights would wait for the
   // weights too).
   load_batch(0);
-  f16x8 wr[RW][NS];
-#pragma unroll
-  for (int r = 0; r < RW; ++r) load_row<NS>(a.w + (int64_t)min(n0 + r, a.N - 1) * K, C, wr[r], lane);
-  const int re = lane < RW * NB ? lane / NB : 0, be = lane < RW * NB ? lane % NB : 0;
-  f16* hp = a.hidden + be * a.h_sb + min(n0 + re, a.N - 1);
-  const float resid = (float)*hp;
+  issue();
   // Keep the loads above in flight together (left alone, the scheduler sinks
   // them next to their uses).
   __builtin_amdgcn_sched_barrier(0);
@@ -583,6 +578,24 @@ __global__ __launch_bounds__(kNT) void attn_merge_gemv_residual_kernel(MergeArgs
     }
   }
   __syncthreads();
+}
+
+template <int NB, int RW>
+__global__ __launch_bounds__(kNT) void attn_merge_gemv_residual_kernel(MergeArgs a) {
+  constexpr int NS = kMaxNormK / 8 / 64;
+  __shared__ __attribute__((aligned(16))) f16 xs[NB * kMaxNormK];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int K = a.K, C = K / 8;
+  const int n0 = (blockIdx.x * kNW + w) * RW;
+  f16x8 wr[RW][NS];
+  const int re = lane < RW * NB ? lane / NB : 0, be = lane < RW * NB ? lane % NB : 0;
+  f16* hp = a.hidden + be * a.h_sb + min(n0 + re, a.N - 1);
+  float resid;
+  merge_partials<NB>(a, xs, [&] {
+#pragma unroll
+    for (int r = 0; r < RW; ++r) load_row<NS>(a.w + (int64_t)min(n0 + r, a.N - 1) * K, C, wr[r], lane);
+    resid = (float)*hp;
+  });
   if (n0 >= a.N) return;
   float acc[RW][NB];
 #pragma unroll
@@ -758,6 +771,51 @@ __global__ __launch_bounds__(kNT) void rms_gate_up_swiglu_mfma_kernel(GateUpArgs
     const float s16 = (float)(f16)(g16 / (1.f + expf(-g16)));
     a.h[col * a.h_sb + jb + t] = (f16)(s16 * u16);
   }
+}
+
+// Merge + o_proj on matrix-core tiles (packed with QF_PACK_PLAIN), for 2-4
+// rows: merge_partials, then one 16-row block per workgroup, its k range split
+// between the four waves (kOpKS) whose partial tiles are added in LDS; the
+// batch rows are the MFMA columns, so a wave spends one MFMA per 1 KB of
+// weights where the row kernel spends four v_dot2 per batch row and 16
+// bytes, plus a 64-lane butterfly per row and batch row.  Lane l finishes
+// rows 16 rb + 4 (l / 16) + i of batch row l % 16: fp16(residual + fp16(acc)).
+// Measured on MI355X at hidden 896 (8 splits at B=1, 4 above), weights past
+// the MALL, row kernel / this one: B=1 2.79 / 3.07 us, B=2 3.31 / 3.14, B=3
+// 3.90 / 3.48, B=4 4.50 / 3.93.
+constexpr int kOpKS = 4;
+constexpr int kOpBlk = kMaxNormK / 32 / kOpKS;
+
+template <int NB>
+__global__ __launch_bounds__(kNT) void attn_merge_o_proj_mfma_kernel(MergeArgs a) {
+  static_assert(kNW / kOpKS == 1, "one row block per workgroup");
+  __shared__ __attribute__((aligned(16))) f16 xs[NB * kMaxNormK];
+  __shared__ f32x4 part[kNW][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int K = a.K, nkb = K / 32;
+  const int per = (nkb + kOpKS - 1) / kOpKS;
+  const int kp = w % kOpKS;
+  const int rb = blockIdx.x;
+  const int kb0 = kp * per, n = min(per, nkb - kb0);
+  const int col = lane & 15, q = lane >> 4;
+  f16* hp = a.hidden + min(col, NB - 1) * a.h_sb + 16 * rb + 4 * q;
+  f16x8 wa[kOpBlk];
+  f16x4 res;
+  merge_partials<NB>(a, xs, [&] {
+#pragma unroll
+    for (int t = 0; t < kOpBlk; ++t) wa[t] = tile_load(a.w, nkb, rb, min(kb0 + t, nkb - 1), lane);
+    res = *reinterpret_cast<const f16x4*>(hp);
+  });
+  f32x4 acc = tile_mfma<NB, kOpBlk>(wa, xs, K, kb0, n, lane);
+  if (kp != 0) part[w][lane] = acc;
+  __syncthreads();
+  if (kp != 0 || col >= NB) return;
+#pragma unroll
+  for (int s = 1; s < kOpKS; ++s) acc += part[w + s][lane];
+  f16x4 o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = (f16)((float)res[i] + (float)(f16)acc[i]);
+  *reinterpret_cast<f16x4*>(hp) = o;
 }
 
 // QKV + bias + RoPE + KV append.  Packing QF_PACK_ROPE makes row block
@@ -1370,13 +1428,18 @@ extern "C" int qf_gemv_residual(const void* inp, int64_t in_sb, const void* w, v
 }
 
 extern "C" int qf_attn_merge_o_proj(const float* acc, const float* m, const float* l, int splits,
-                                    int KVH, int G, const void* w_o, void* hidden, int64_t h_sb,
-                                    int B, int N, void* stream) {
+                                    int KVH, int G, const void* w_o, int w_layout, void* hidden,
+                                    int64_t h_sb, int B, int N, void* stream) {
   const int K = KVH * G * kHeadDim;
+  if (w_layout != QF_W_ROWS && w_layout != QF_W_TILES) return QF_ERR_INVALID_ARG;
   if (B < 1 || B > kMaxB || G < 1 || KVH < 1 || K > kMaxNormK || KVH * G * 16 > kNT)
     return QF_ERR_UNSUPPORTED;
   if (!acc || !m || !l || !w_o || !hidden || N < 1 || splits < 1) return QF_ERR_INVALID_ARG;
   if (!al16(acc) || !al16(w_o)) return QF_ERR_INVALID_ARG;
+  // Matrix-core form: whole 16-row blocks, 8-byte residual loads and stores.
+  if (w_layout == QF_W_TILES && N % 16) return QF_ERR_UNSUPPORTED;
+  if (w_layout == QF_W_TILES && ((reinterpret_cast<uintptr_t>(hidden) & 7) || (h_sb & 3)))
+    return QF_ERR_INVALID_ARG;
   MergeArgs a;
   a.acc = acc; a.m = m; a.l = l;
   a.splits = splits; a.KVH = KVH; a.G = G;
@@ -1386,9 +1449,14 @@ extern "C" int qf_attn_merge_o_proj(const float* acc, const float* m, const floa
   hipStream_t st = static_cast<hipStream_t>(stream);
   // Every workgroup re-reads all partials, so batched calls use fewer, wider
   // workgroups (measured on MI355X: B=1 best at 2 rows per wave, B=4 at 4).
+  const size_t shm = 0;
+  if (w_layout == QF_W_TILES) {
+    const dim3 grid(N / 16), block(kNT);
+    QF_DISPATCH_B(B, attn_merge_o_proj_mfma_kernel)
+    return (int)hipGetLastError();
+  }
   const int RW = B == 1 ? 2 : 4;
   const dim3 grid((N + kNW * RW - 1) / (kNW * RW)), block(kNT);
-  const size_t shm = 0;
   if (RW == 2) { QF_DISPATCH_B(B, attn_merge_gemv_residual_kernel, 2) }
   else { QF_DISPATCH_B(B, attn_merge_gemv_residual_kernel, 4) }
   return (int)hipGetLastError();

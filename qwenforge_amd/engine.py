@@ -116,6 +116,7 @@ class DecodeEngine:
         self.tile_weights = tile_weights
         self._tiles = None
         self._lm_tiles = None
+        self._o_tiles = None
         self._ctx = None
         self.graphs = GraphRegistry()
         self.captures = 0  # graph captures so far (registry hits capture nothing)
@@ -138,6 +139,18 @@ class DecodeEngine:
                             step_ops.pack_weight(l["gate_up_weight"], step_ops.PACK_SWIGLU))
                            for l in self.w["layers"]]
         return self._tiles[i]
+
+    def o_proj_weight(self, i: int, batch: int):
+        """The o_proj weight of layer i for the fused step's merge + o_proj at
+        ``batch`` rows: row-major, or its ``step_ops.Tiles`` from
+        TILE_MIN_BATCH rows (packed once, on first use)."""
+        w = self.w["layers"][i]["o_weight"]
+        if not self.tile_weights or batch < self.TILE_MIN_BATCH or w.shape[0] % 16:
+            return w
+        if self._o_tiles is None:
+            self._o_tiles = [step_ops.pack_weight(l["o_weight"], step_ops.PACK_PLAIN)
+                             for l in self.w["layers"]]
+        return self._o_tiles[i]
 
     # Rows from which the fused step's lm_head reads matrix-core tiles:
     # measured on MI355X at vocab 151936, 45.6-45.8 us per call at any batch
@@ -286,7 +299,7 @@ class DecodeEngine:
             # Split-K partials; their merge is the o_proj kernel's prologue.
             ops.flash_decode_split(grouped, kc, vc, ctx["bias"], ctx["flash"],
                                    kv_last=ctx["write"], scale=self.scale)
-            step_ops.attn_merge_o_proj(ctx["flash"], layer["o_weight"], hidden)
+            step_ops.attn_merge_o_proj(ctx["flash"], self.o_proj_weight(i, b), hidden)
             step_ops.rms_gate_up_swiglu(hidden, layer["post_norm"], eps, w_gate_up, h)
             step_ops.gemv_residual(h, layer["down_weight"], hidden)
         step_ops.rms_lm_head(hidden, self.w["final_norm"], eps, self.lm_head_weight(b), ctx["logits"],

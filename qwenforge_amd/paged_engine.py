@@ -127,7 +127,7 @@ class PagedDecodeEngine(DecodeEngine):
             # The slot just written is the row's last valid one.
             paged.flash_decode_split_paged(grouped, kp, vp, table, None, ctx["flash"], kv_last=pos,
                                            scale=self.scale)
-            step_ops.attn_merge_o_proj(ctx["flash"], layer["o_weight"], hidden)
+            step_ops.attn_merge_o_proj(ctx["flash"], self.o_proj_weight(i, b), hidden)
             step_ops.rms_gate_up_swiglu(hidden, layer["post_norm"], eps, w_gate_up, h)
             step_ops.gemv_residual(h, layer["down_weight"], hidden)
         step_ops.rms_lm_head(hidden, self.w["final_norm"], eps, self.lm_head_weight(b), ctx["logits"],

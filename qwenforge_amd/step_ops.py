@@ -203,12 +203,14 @@ def gemv_residual(inp: torch.Tensor, w: torch.Tensor, hidden: torch.Tensor) -> N
     _lib.check(rc, "qf_gemv_residual")
 
 
-def attn_merge_o_proj(flash, w_o: torch.Tensor, hidden: torch.Tensor) -> None:
+def attn_merge_o_proj(flash, w_o, hidden: torch.Tensor) -> None:
     """hidden <- fp16(hidden + fp16(merge(flash partials) @ w_o^T)), in place.
 
     ``flash`` is the decode scratch filled by ``ops.flash_decode_split``:
     acc (B, KVH, S, G, 64), m and l (B, KVH, S, G), fp32 contiguous.  The
     merge replaces the combine launch (SE:117-162); see include/qf_step.h.
+    ``w_o``: the (hidden, KVH*G*64) weight, or its ``Tiles`` packed with
+    PACK_PLAIN (matrix-core kernel).
     """
     acc, m, l = flash[:3]
     b, kvh, splits, g, d = acc.shape
@@ -220,10 +222,10 @@ def attn_merge_o_proj(flash, w_o: torch.Tensor, hidden: torch.Tensor) -> None:
     if d != HEAD_DIM or m.shape != (b, kvh, splits, g) or l.shape != m.shape:
         raise ValueError("flash partials must be (B, KVH, S, G, 64) / (B, KVH, S, G)")
     n = w_o.shape[0]
-    _weight("w_o", w_o, n, kvh * g * d)
+    w_ptr, w_layout = _weight("w_o", w_o, n, kvh * g * d, PACK_PLAIN)
     h_sb = _rows("hidden", hidden, b, n)
     rc = _lib.load().qf_attn_merge_o_proj(acc.data_ptr(), m.data_ptr(), l.data_ptr(), splits,
-                                          kvh, g, w_o.data_ptr(), hidden.data_ptr(), h_sb, b, n,
+                                          kvh, g, w_ptr, w_layout, hidden.data_ptr(), h_sb, b, n,
                                           _stream(hidden.device))
     _lib.check(rc, "qf_attn_merge_o_proj")
 

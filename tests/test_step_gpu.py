@@ -230,8 +230,10 @@ def test_lm_head_random_logits_close(dev, batch, tiles):
 
 @pytest.mark.parametrize("batch", [1, 2, 3, 4])
 @pytest.mark.parametrize("splits", [1, 5, 18])
-def test_attn_merge_o_proj(dev, batch, splits):
-    """Split-K partials merged in the o_proj prologue == oracle attention + o_proj."""
+@pytest.mark.parametrize("tiles", [False, True])
+def test_attn_merge_o_proj(dev, batch, splits, tiles):
+    """Split-K partials merged in the o_proj prologue == oracle attention +
+    o_proj, for the row kernel and the matrix-core kernel (packed weight)."""
     import oracle
     from qwenforge_amd import ops, workloads
 
@@ -243,9 +245,11 @@ def test_attn_merge_o_proj(dev, batch, splits):
     w_o = _rand(HIDDEN, HIDDEN, gen=gen, std=0.02)
     res = _rand(batch, HIDDEN, gen=gen)
     hidden = res.to(dev)
-    print(f"[merge+o_proj] B={batch} S={splits}", flush=True)
+    print(f"[merge+o_proj] B={batch} S={splits} tiles={tiles}", flush=True)
     ops.flash_decode_split(c.grouped, c.key_cache, c.value_cache, None, flash, kv_last=kv_last)
-    step_ops.attn_merge_o_proj(flash, w_o.to(dev), hidden)
+    wd = w_o.to(dev)
+    step_ops.attn_merge_o_proj(flash, step_ops.pack_weight(wd, step_ops.PACK_PLAIN) if tiles else wd,
+                               hidden)
     # The unfused pair: combine launch, then the plain GEMV.
     out = ops.flash_decode_combine(flash)
     hidden2 = res.to(dev)
