@@ -120,7 +120,7 @@ def test_rms_qkv_gathers_embedding_rows_and_skips_out_of_range_slot(dev, tiles):
 
 @pytest.mark.parametrize("batch", [1, 2, 3, 4])
 @pytest.mark.parametrize("k_dim,n", [(HIDDEN, HIDDEN), (INTER, HIDDEN), (200, 72), (6144, 96),
-                                     (8192, 64)])
+                                     (8192, 64), (1032, 97), (5128, 40)])
 @pytest.mark.parametrize("integer", [True, False])
 def test_gemv_residual(dev, batch, k_dim, n, integer):
     gen = torch.Generator().manual_seed(k_dim + n + batch)
