@@ -353,3 +353,22 @@ def test_short_generations_run_the_step_eagerly(dev):
     assert eng.captures == 0 and len(eng.graphs) == 0
     full = DecodeEngine(cfg, w, dev).generate(ids, 8)
     assert torch.equal(short, full[:, :4]) and torch.equal(one, full[:, :1])
+
+
+def test_registry_evicts_past_its_budget(dev):
+    """With a budget below one entry's caches, each new shape evicts the
+    previous one (the newest always stays, SE:1099-1103); coming back to an
+    evicted shape captures again, and its tokens still equal a fresh engine's."""
+    cfg = Qwen2Config(layers=2)
+    w = init_weights(cfg, dev, seed=8)
+    eng = DecodeEngine(cfg, w, dev)
+    eng.graphs.byte_budget = 1
+    gen = torch.Generator().manual_seed(9)
+    a = torch.randint(0, cfg.vocab, (1, 100), generator=gen).to(dev)   # capacity 128
+    c = torch.randint(0, cfg.vocab, (1, 150), generator=gen).to(dev)   # capacity 192
+    eng.generate(a, 10)
+    eng.generate(c, 10)
+    assert eng.graphs.keys() == [(1, 192, False)] and eng.captures == 2
+    got = eng.generate(a, 10)
+    assert eng.graphs.keys() == [(1, 128, False)] and eng.captures == 3
+    assert torch.equal(got, DecodeEngine(cfg, w, dev).generate(a, 10))
