@@ -77,26 +77,37 @@ def test_config2_ragged_24_layers(dev, use_kv_last):
 
 @pytest.mark.parametrize("batch,length", [(1, 8192), (2, 4096), (4, 8192), (8, 2048), (8, 4096),
                                           (3, 5000), (1, 2500), (8, 512)])
-def test_decode_plan_shapes_match_oracle(dev, batch, length):
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_decode_plan_shapes_match_oracle(dev, batch, length, with_bias):
     """The default plan (ops.decode_plan) at the shapes where it picks split +
     combine launches with 16-128 splits (one workgroup per CU, or fewer
     64-key splits) or a capped single launch; rows ragged through kv_last,
-    stale NaN past each row's last slot."""
+    stale NaN past each row's last slot, and optionally a bias with holes
+    inside the valid range (fp16-min, as the reference masks padding)."""
     case = workloads.decode_uniform(batch, length, seed=length + batch)
     gen = torch.Generator().manual_seed(batch)
     lengths = torch.randint(length // 2, length + 1, (batch,), generator=gen).tolist()
     for b, n in enumerate(lengths):
         case.key_cache[b, :, n:] = float("nan")
         case.value_cache[b, :, n:] = float("nan")
+    bias = None
+    if with_bias:
+        bias = torch.zeros(batch, length, dtype=torch.float16)
+        bias[torch.rand(batch, length, generator=gen) < 0.1] = oracle.FP16_MIN
+        for b, n in enumerate(lengths):
+            bias[b, n - 1] = 0.0  # at least one valid slot per row
+        case.bias = bias
     kv_last = torch.tensor([n - 1 for n in lengths], dtype=torch.int64, device=dev)
     splits, fused = ops.decode_plan(batch, 2, length)
-    print(f"[decode plan B={batch} L={length}] splits={splits} fused={fused}", flush=True)
+    print(f"[decode plan B={batch} L={length} bias={with_bias}] splits={splits} fused={fused}",
+          flush=True)
     out, flash = _run(case, dev, kv_last=kv_last)
     assert flash[0].shape[2] == splits and (len(flash) > 4) == fused
     worst = 0.0
     for b, n in enumerate(lengths):
         ref = oracle.grouped_decode_attention(case.grouped[b:b + 1], case.key_cache[b:b + 1, :, :n],
-                                              case.value_cache[b:b + 1, :, :n], None)
+                                              case.value_cache[b:b + 1, :, :n],
+                                              None if bias is None else bias[b:b + 1, :n])
         worst = max(worst, _err(out[b:b + 1], ref))
     assert worst <= TOL
 
