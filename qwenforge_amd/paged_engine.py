@@ -94,7 +94,8 @@ class PagedDecodeEngine(DecodeEngine):
             ctx["hidden"] = torch.zeros(batch, cfg.hidden, device=dev, dtype=f16)
             ctx["q_rot"] = torch.zeros(batch, cfg.heads, cfg.head_dim, device=dev, dtype=f16)
             ctx["h"] = torch.zeros(batch, cfg.intermediate, device=dev, dtype=f16)
-            ctx["keys"] = torch.zeros(batch, step_ops.LM_BLOCKS, device=dev, dtype=torch.long)
+            ctx["keys"] = torch.zeros(batch, step_ops.lm_blocks(self.lm_head_weight(batch)),
+                                      device=dev, dtype=torch.long)
         return ctx
 
     def _step(self, ctx):

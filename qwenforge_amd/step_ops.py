@@ -29,8 +29,16 @@ from .ops import _ptr, _stream
 
 MAX_BATCH = 4
 HEAD_DIM = 64
-# lm_head blocks: four per CU on the 256-CU part.
+# lm_head workgroups (the width of the argmax keys): four per CU on the 256-CU
+# part for the row kernel, two for the matrix-core kernel (measured on MI355X
+# at vocab 151936, B=4: 44.3 us at 512 workgroups, 45.9 at 1024, 48.0 at 256).
 LM_BLOCKS = 1024
+LM_TILE_BLOCKS = 512
+
+
+def lm_blocks(w_lm) -> int:
+    """Workgroups (argmax key columns) for an lm_head call with ``w_lm``."""
+    return LM_TILE_BLOCKS if isinstance(w_lm, Tiles) else LM_BLOCKS
 
 # Weight layouts and packing row maps (include/qf_step.h).
 W_ROWS, W_TILES = 0, 1
