@@ -76,12 +76,13 @@ def test_config2_ragged_24_layers(dev, use_kv_last):
 
 
 @pytest.mark.parametrize("batch,length", [(1, 8192), (2, 4096), (4, 8192), (8, 2048), (8, 4096),
-                                          (3, 5000), (1, 2500), (8, 512)])
+                                          (3, 5000), (1, 2500), (8, 512), (1, 200), (4, 256)])
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_decode_plan_shapes_match_oracle(dev, batch, length, with_bias):
     """The default plan (ops.decode_plan) at the shapes where it picks split +
     combine launches with 16-128 splits (one workgroup per CU, or fewer
-    64-key splits) or a capped single launch; rows ragged through kv_last,
+    64-key splits), a capped single launch, or one split for rows of at most
+    256 slots; rows ragged through kv_last,
     stale NaN past each row's last slot, and optionally a bias with holes
     inside the valid range (fp16-min, as the reference masks padding)."""
     case = workloads.decode_uniform(batch, length, seed=length + batch)

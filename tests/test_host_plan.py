@@ -11,6 +11,10 @@ from qwenforge_amd import ops
 
 
 @pytest.mark.parametrize("batch,length,splits,fused", [
+    (1, 128, 1, False),      # one split, no merge: 3.73 us vs 5.27 for 4 fused splits
+    (1, 256, 1, False),      # 4.82 us vs 5.35 for 8 fused splits
+    (8, 256, 1, False),      # 4.99 us vs 6.02 for 4 fused splits
+    (1, 320, 10, True),      # from 320 slots the single-launch merge wins (5.54 at 8 vs 5.80 at 1)
     (1, 512, 16, True),      # config 1: 32-key splits, single launch (5.46 us vs 5.58 at 8)
     (1, 2048, 16, True),     # 128-key splits: 6.23 us vs 6.47 for 64 split + combine
     (2, 512, 8, True),       # 6.23 us vs 6.58 at 4
@@ -45,10 +49,12 @@ def test_decode_plan_at_benchmark_shapes(batch, length, splits, fused):
 
 @pytest.mark.parametrize("batch", list(range(1, 129)))
 def test_workgroup_counts_stay_in_the_measured_ranges(batch):
-    for length in (512, 1024, 2048, 4096, 5760, 8192, 16384, 32768):
+    for length in (64, 256, 320, 512, 1024, 2048, 4096, 5760, 8192, 16384, 32768):
         s, fused = ops.decode_plan(batch, 2, length)
         pairs, wg = 2 * batch, 2 * batch * s
         assert 1 <= s <= 128
+        if length <= 256 and pairs <= 16:
+            assert (s, fused) == (1, False)  # one split per (b, kv head), no merge
         assert fused == (s > 1 and (pairs > 16 and s <= 32 or pairs <= 16 and fused))
         if fused:
             assert s <= 32  # the single-launch merge folds <= 8 partials per lane
