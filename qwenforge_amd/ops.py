@@ -63,16 +63,19 @@ def decode_plan(batch: int, kv_heads: int, length: int) -> tuple[int, bool]:
     """(split count, single-launch merge) for a decode call over rows of
     ``length`` slots on MI355X (256 CUs).
 
-    Up to 16 (b, kv head) pairs (measured on MI355X, graph-replayed calls
+    Rows of at most 256 slots, any number of (b, kv head) pairs: one split,
+    no merge (one workgroup per pair whose waves take a 32-key tile each and
+    merge in LDS) -- measured on MI355X: B=1, L=128: 3.73 us against 5.27 for
+    4 fused splits; B=1, L=256: 4.82 against 5.35 for 8; B=8, L=256: 4.99
+    against 6.02 for 4; 24 pairs, L=256: 5.00 against 6.29 for 2; 64 pairs,
+    L=256: 5.14 against 6.57 for 2 (from 320 slots the single-launch merge
+    wins: B=1, L=320: 5.54 for 8 fused splits against 5.80; 24 pairs,
+    L=512: 6.59 for 4 against 7.08).
+
+    Longer rows, up to 16 pairs (measured on MI355X, graph-replayed calls
     over caches rotated past the MALL, every split count from 4 to 256 in both
     merge modes at 1-8 rows and 512-32768 slots):
 
-    * rows of at most 256 slots (up to 16 pairs): one split, no merge (one workgroup per (b,
-      kv head) whose waves take a 32-key tile each and merge in LDS) -- e.g.
-      B=1, L=128: 3.73 us against 5.27 for 4 fused splits; B=1, L=256: 4.82
-      against 5.35 for 8; B=8, L=256: 4.99 against 6.02 for 4 (from 320
-      slots the single-launch merge wins: B=1, L=320: 5.54 for 8 fused
-      splits against 5.80);
     * short rows (``length <= 2048`` with at most 8 pairs, or ``<= 512``):
       the single-launch merge.  With at most 8 pairs, splits of 32 keys (64
       with more than 2 pairs), at most 16 -- e.g. config 1 (B=1, L=512): 16
@@ -92,16 +95,16 @@ def decode_plan(batch: int, kv_heads: int, length: int) -> tuple[int, bool]:
       form here: the combine launch now costs less than the single-launch
       merge's serial tail.
 
-    More pairs: one workgroup per CU (``_fill_splits``), single launch.  (The reference's
+    Longer rows, more pairs: one workgroup per CU (``_fill_splits``), single launch.  (The reference's
     rule, ``max(1, min(32, 272 // (B*KVH), cap // 256))`` at SE:1027, targets
     68 SMs and always uses two launches.)
     """
     pairs = max(1, batch * kv_heads)
+    if length <= 256:
+        return 1, False
     if pairs > 16:
         s = _fill_splits(pairs, length)
         return s, prefer_fused(s)
-    if length <= 256:
-        return 1, False
     if pairs <= 8 and length <= 2048:
         keys = 32 if pairs <= 2 else 64
         s = max(1, min(math.ceil(length / keys), 16))

@@ -76,7 +76,7 @@ def test_config2_ragged_24_layers(dev, use_kv_last):
 
 
 @pytest.mark.parametrize("batch,length", [(1, 8192), (2, 4096), (4, 8192), (8, 2048), (8, 4096),
-                                          (3, 5000), (1, 2500), (8, 512), (1, 200), (4, 256)])
+                                          (3, 5000), (1, 2500), (8, 512), (1, 200), (4, 256), (12, 256)])
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_decode_plan_shapes_match_oracle(dev, batch, length, with_bias):
     """The default plan (ops.decode_plan) at the shapes where it picks split +

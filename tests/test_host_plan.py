@@ -14,6 +14,10 @@ from qwenforge_amd import ops
     (1, 128, 1, False),      # one split, no merge: 3.73 us vs 5.27 for 4 fused splits
     (1, 256, 1, False),      # 4.82 us vs 5.35 for 8 fused splits
     (8, 256, 1, False),      # 4.99 us vs 6.02 for 4 fused splits
+    (12, 256, 1, False),     # 24 pairs: 5.00 us vs 6.29 for 2 fused splits
+    (32, 256, 1, False),     # 64 pairs: 5.14 us vs 6.57 for 2 fused splits
+    (32, 128, 1, False),     # 4.19 us vs 6.02 for 2 fused splits
+    (12, 512, 4, True),      # 24 pairs: 6.59 us vs 7.08 for one split
     (1, 320, 10, True),      # from 320 slots the single-launch merge wins (5.54 at 8 vs 5.80 at 1)
     (1, 512, 16, True),      # config 1: 32-key splits, single launch (5.46 us vs 5.58 at 8)
     (1, 2048, 16, True),     # 128-key splits: 6.23 us vs 6.47 for 64 split + combine
@@ -53,7 +57,7 @@ def test_workgroup_counts_stay_in_the_measured_ranges(batch):
         s, fused = ops.decode_plan(batch, 2, length)
         pairs, wg = 2 * batch, 2 * batch * s
         assert 1 <= s <= 128
-        if length <= 256 and pairs <= 16:
+        if length <= 256:
             assert (s, fused) == (1, False)  # one split per (b, kv head), no merge
         assert fused == (s > 1 and (pairs > 16 and s <= 32 or pairs <= 16 and fused))
         if fused:
