@@ -77,6 +77,22 @@ def test_decode_launch_plan_names_the_kernel():
     assert _lib.load().qf_decode_waves(1, 2, 0, 512, 1, 0) == -1
 
 
+@pytest.mark.parametrize("b,cap,splits,fused,waves", [
+    (1, 512, 16, 1, 8),      # config 1: the single-launch merge gives each of 7 queries a wave
+    (4, 2048, 16, 1, 8),     # config 2: same, although each split has only 4 tiles
+    (1, 32768, 128, 0, 4),   # config 3: 256 workgroups, 8 tiles each -> two tiles per wave
+    (4, 4096, 32, 0, 4),     # 256 workgroups, 4 tiles each -> four waves
+    (1, 256, 1, 0, 8),       # one split over 2 workgroups: one tile per wave
+    (12, 256, 1, 0, 4),      # one split over 24 workgroups: at least two tiles per wave
+    (16, 32768, 8, 1, 8),    # bandwidth regime, one workgroup per CU
+    (64, 4096, 2, 1, 8),
+    (12, 5760, 10, 1, 8),    # the reference's benchmark shape
+])
+def test_decode_waves_at_benchmark_shapes(b, cap, splits, fused, waves):
+    """Waves per decode workgroup as the library launches them (host code, no GPU)."""
+    assert _lib.load().qf_decode_waves(b, 2, 7, cap, splits, fused) == waves
+
+
 def test_stream_read_rejects_bad_arguments():
     lib = _lib.load()
     assert lib.qf_stream_read(None, 1024, 16, 4, None) == -1
