@@ -78,6 +78,9 @@ int qf_abi_version(void);
  *          meaning (unnormalised sum p*v, running max in natural-log units,
  *          sum p).  Split s covers [s*split_len, min(+split_len, upper)) with
  *          split_len = ceil(upper / S) rounded up to a multiple of 32.
+ *          With splits = 1 one workgroup per (b, kv head) covers every slot,
+ *          merges its waves in LDS and writes `out` itself: acc, m, l and the
+ *          ticket are not read or written.
  *   ticket NULL: the merge runs as a second kernel (reference two-launch
  *          shape).  Non-NULL: int32[B*KVH], one counter per (b, kv head),
  *          zero-filled once by the caller; the merge runs inside the same
