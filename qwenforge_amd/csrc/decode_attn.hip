@@ -156,10 +156,14 @@ __device__ __forceinline__ void lse_merge_lanes(float& M, float& L, f32x4& A) {
 // loads each of its 4 kB partials' (m, l) once -- lane i loads partial
 // sub0 + i % 4 + nsub * (i / 4) -- and hands them to the 16 lanes that fold
 // the partial with ds_bpermute; the acc slices are one 16-byte load per lane
-// and partial, at a uniform distance (scalar offset) from the first.  So a
-// batch is 2 + kB vector memory instructions per wave, all in flight before
-// the first wait: one round trip.  (Sixteen lanes loading each (m, l) would
-// make it 2 kB more, and the merge is bound by those instructions.)
+// and partial.  So a batch is 2 + kB vector memory instructions per wave, all
+// in flight before the first wait: one round trip.  (Sixteen lanes loading
+// each (m, l) would make it 2 kB more, and the merge is bound by those
+// instructions.)  Every partial index goes into the vector offset: the buffer
+// range check covers the vector and immediate offsets but not the scalar
+// offset, and only the checked offset turns a partial past S (the last
+// batch of a split count that is not a multiple of nsub * kB) into zeros
+// instead of a read of whatever follows the scratch.
 // kCoherent: sc1 loads, for partials that other workgroups of the same
 // launch stored with sc1 stores.
 template <int kB, bool kCoherent>
@@ -177,7 +181,8 @@ __device__ __forceinline__ void fold_wave(const DecodeArgs& a, int bh, int q, in
   const int j_ml = sub0 + (ml_lane & 3) + nsub * (ml_lane >> 2);
   const int acc_step = nsub * G * kD * 4;
   for (int j0 = 0; j0 < S; j0 += nsub * kB) {
-    // Partials past S read 0 (the buffers end there) and are masked below.
+    // Partials past S read 0 (the buffers end there; the offsets are all
+    // vector offsets, which the range check covers) and are masked below.
     const float m_mine = __builtin_bit_cast(
         float, __builtin_amdgcn_raw_buffer_load_b32(rm, ((j0 + j_ml) * G + q) * 4, 0, aux));
     const float l_mine = __builtin_bit_cast(
@@ -187,7 +192,7 @@ __device__ __forceinline__ void fold_wave(const DecodeArgs& a, int bh, int q, in
 #pragma unroll
     for (int u = 0; u < kB; ++u)
       av[u] = __builtin_bit_cast(
-          f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, acc_off, u * acc_step, aux));
+          f32x4, __builtin_amdgcn_raw_buffer_load_b128(ra, acc_off + u * acc_step, 0, aux));
     // Keep every load of the batch above this point: left alone, the
     // scheduler sinks loads next to their uses, and the batch becomes a chain
     // of dependent round trips.
@@ -873,23 +878,43 @@ __global__ __launch_bounds__(256) void zero_counters_kernel(int32_t* p, int n) {
   for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) p[i] = 0;
 }
 
-// Device address of this GPU's `scratch` (the current device's).  The first
-// call on a device looks it up and zeroes the counters on `st` with a fill
-// kernel (legal under stream capture, where a memset node is not wanted).
+// Device address of `scratch` on the GPU that owns `st` (the null stream
+// belongs to the current device).  The first call on a device looks the
+// address up with that device current and zeroes the counters on `st` with a
+// fill kernel, not a memset node: when that first call happens under stream
+// capture the fill is recorded into the caller's graph and runs again at
+// every replay, which is harmless because every merge leaves its counter at
+// zero (and the array is zero when the library loads).
 int noalloc_base(hipStream_t st, unsigned char** base) {
   int dev = -1;
-  hipError_t e = hipGetDevice(&dev);
+  hipError_t e;
+  if (st == nullptr) {
+    e = hipGetDevice(&dev);
+  } else {
+    hipDevice_t d = -1;
+    e = hipStreamGetDevice(st, &d);
+    dev = (int)d;
+  }
   if (e != hipSuccess) return (int)e;
   if (dev < 0 || dev >= kMaxDevices) return QF_ERR_UNSUPPORTED;
   std::lock_guard<std::mutex> lock(g_noalloc_mu);
   if (g_noalloc_base[dev] == nullptr) {
+    int cur = -1;
+    e = hipGetDevice(&cur);
+    if (e != hipSuccess) return (int)e;
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return (int)e;
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (e != hipSuccess) return (int)e;
-    if (p == nullptr) return (int)hipErrorInvalidSymbol;
-    hipLaunchKernelGGL(zero_counters_kernel, dim3(64), dim3(256), 0, st,
-                       reinterpret_cast<int32_t*>(p), kNoAllocCounters);
-    e = hipGetLastError();
+    if (e == hipSuccess && p == nullptr) e = hipErrorInvalidSymbol;
+    if (e == hipSuccess) {
+      hipLaunchKernelGGL(zero_counters_kernel, dim3(64), dim3(256), 0, st,
+                         reinterpret_cast<int32_t*>(p), kNoAllocCounters);
+      e = hipGetLastError();
+    }
+    if (cur != dev) {
+      const hipError_t r = hipSetDevice(cur);
+      if (e == hipSuccess) e = r;
+    }
     if (e != hipSuccess) return (int)e;
     g_noalloc_base[dev] = static_cast<unsigned char*>(p);
   }

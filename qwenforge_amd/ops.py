@@ -29,8 +29,24 @@ from . import _lib
 
 HEAD_DIM = 64
 MAX_GROUPS = 16
-# MI355X: 256 compute units in 8 XCDs.
+# MI355X: 256 compute units in 8 XCDs.  The planner reads the count from the
+# device (a partitioned MI355X exposes fewer); this is the value it assumes
+# where no device is visible (host-side planning, CPU tests).
 NUM_CUS = 256
+_CU_COUNT: dict = {}
+
+
+def num_cus(device=None) -> int:
+    """Compute units of ``device`` (default: the current HIP device), read once
+    per device from its properties; ``NUM_CUS`` when no GPU is visible."""
+    if not torch.cuda.is_available():
+        return NUM_CUS
+    idx = torch.cuda.current_device() if device is None else torch.device(device).index
+    if idx is None:
+        idx = torch.cuda.current_device()
+    if idx not in _CU_COUNT:
+        _CU_COUNT[idx] = int(torch.cuda.get_device_properties(idx).multi_processor_count)
+    return _CU_COUNT[idx]
 
 
 def _stream(device: torch.device) -> int:
@@ -59,9 +75,14 @@ def _require_cuda_fp16(name: str, t: torch.Tensor, ndim: int | None = None) -> N
 # decode
 # --------------------------------------------------------------------------
 
-def decode_plan(batch: int, kv_heads: int, length: int) -> tuple[int, bool]:
+def decode_plan(batch: int, kv_heads: int, length: int,
+                cus: int | None = None) -> tuple[int, bool]:
     """(split count, single-launch merge) for a decode call over rows of
-    ``length`` slots on MI355X (256 CUs).
+    ``length`` slots on a device with ``cus`` compute units (default: the
+    current device's, ``num_cus()``; 256 on a whole MI355X, where every figure
+    below was measured).  The workgroup bounds scale with the CU count: one
+    workgroup per CU for split + combine, three per four CUs for the capped
+    single launch, and the one-workgroup-per-CU fill past ``cus / 16`` pairs.
 
     Rows of at most 256 slots, any number of (b, kv head) pairs: one split,
     no merge (one workgroup per pair whose waves take a 32-key tile each and
@@ -99,26 +120,27 @@ def decode_plan(batch: int, kv_heads: int, length: int) -> tuple[int, bool]:
     rule, ``max(1, min(32, 272 // (B*KVH), cap // 256))`` at SE:1027, targets
     68 SMs and always uses two launches.)
     """
+    cus = num_cus() if cus is None else max(1, int(cus))
     pairs = max(1, batch * kv_heads)
     if length <= 256:
         return 1, False
-    if pairs > 16:
-        s = _fill_splits(pairs, length)
+    if pairs > max(1, cus // 16):
+        s = _fill_splits(pairs, length, target_workgroups=cus)
         return s, prefer_fused(s)
     if pairs <= 8 and length <= 2048:
         keys = 32 if pairs <= 2 else 64
-        s = max(1, min(math.ceil(length / keys), 16))
+        s = max(1, min(math.ceil(length / keys), 16, max(1, 3 * cus // 4 // pairs)))
         return s, s > 1
     if length <= 512:
-        s = max(1, min(math.ceil(length / 128), 192 // pairs, 32))
+        s = max(1, min(math.ceil(length / 128), 3 * cus // 4 // pairs, 32))
         return s, s > 1
-    s = max(1, min(NUM_CUS // pairs, 128, math.ceil(length / 64)))
+    s = max(1, min(cus // pairs, 128, math.ceil(length / 64)))
     return s, False
 
 
-def choose_splits(batch: int, kv_heads: int, length: int) -> int:
+def choose_splits(batch: int, kv_heads: int, length: int, cus: int | None = None) -> int:
     """Split count of ``decode_plan``."""
-    return decode_plan(batch, kv_heads, length)[0]
+    return decode_plan(batch, kv_heads, length, cus)[0]
 
 
 def _fill_splits(pairs: int, length: int, min_keys: int = 128,
@@ -160,7 +182,7 @@ def make_flash_scratch(batch: int, kv_heads: int, groups: int, capacity: int,
     be captured into a hipGraph.
     """
     if splits is None:
-        splits, planned = decode_plan(batch, kv_heads, capacity)
+        splits, planned = decode_plan(batch, kv_heads, capacity, num_cus(device))
         fused = planned if fused is None else fused
     fused = prefer_fused(splits) if fused is None else fused
     f32 = dict(device=device, dtype=torch.float32)

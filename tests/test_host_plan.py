@@ -47,14 +47,14 @@ from qwenforge_amd import ops
     (128, 1024, 1, False),   # 256 pairs: one split per row fills the chip, no merge
 ])
 def test_decode_plan_at_benchmark_shapes(batch, length, splits, fused):
-    assert ops.decode_plan(batch, 2, length) == (splits, fused)
-    assert ops.choose_splits(batch, 2, length) == splits
+    assert ops.decode_plan(batch, 2, length, cus=256) == (splits, fused)
+    assert ops.choose_splits(batch, 2, length, cus=256) == splits
 
 
 @pytest.mark.parametrize("batch", list(range(1, 129)))
 def test_workgroup_counts_stay_in_the_measured_ranges(batch):
     for length in (64, 256, 320, 512, 1024, 2048, 4096, 5760, 8192, 16384, 32768):
-        s, fused = ops.decode_plan(batch, 2, length)
+        s, fused = ops.decode_plan(batch, 2, length, cus=256)
         pairs, wg = 2 * batch, 2 * batch * s
         assert 1 <= s <= 128
         if length <= 256:
@@ -77,6 +77,32 @@ def test_workgroup_counts_stay_in_the_measured_ranges(batch):
             assert wg <= ops.NUM_CUS, (batch, length, s)
         # Splits keep at least one 32-key tile.
         assert -(-length // s) >= 32
+
+
+@pytest.mark.parametrize("cus", [32, 64, 80, 128, 304])
+def test_plan_follows_the_device_cu_count(cus):
+    """A partitioned MI355X (e.g. 32 CUs per partition) or another part: no
+    plan puts more workgroups on the device than it has CUs (one per CU for
+    split + combine and the fill rule, three per four CUs for the capped
+    single launch), and the count comes from the device when none is given."""
+    for batch in (1, 2, 4, 8, 16, 64):
+        for length in (320, 512, 2048, 4096, 32768):
+            s, fused = ops.decode_plan(batch, 2, length, cus=cus)
+            wg = 2 * batch * s
+            assert s >= 1
+            if s > 1:
+                assert wg <= cus, (cus, batch, length, s)
+            if fused and 2 * batch <= max(1, cus // 16):
+                assert wg <= 3 * cus // 4 or s == 1, (cus, batch, length, s)
+
+
+def test_plan_reads_the_cu_count_from_the_device(monkeypatch):
+    """ops.num_cus() is the default: a stubbed device with 64 CUs gives the
+    64-CU plan (config 3: 32 splits per kv head instead of 128)."""
+    monkeypatch.setattr(ops, "num_cus", lambda device=None: 64)
+    assert ops.decode_plan(1, 2, 32768) == ops.decode_plan(1, 2, 32768, cus=64)
+    assert ops.decode_plan(1, 2, 32768)[0] * 2 <= 64
+    assert ops.decode_plan(1, 2, 32768, cus=256) != ops.decode_plan(1, 2, 32768)
 
 
 def test_engine_capacity_rule_equals_oracle():
