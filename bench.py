@@ -41,13 +41,22 @@ def _args():
     p.add_argument("--warmup", type=int, default=20)
     p.add_argument("--no-extras", action="store_true", help="headline line only")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    p.add_argument("--cpu-seconds", type=float, default=16.0,
+    p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="time budget of the attention rows of the CPU baseline (all threads; "
                         "the one-thread rows take a third more)")
     p.add_argument("--prefill-only", action="store_true",
                    help="time only the config-4 prefill leg (for kernel profiles)")
-    p.add_argument("--only", choices=("cfg1", "cfg2", "cfg3", "prefill", "e2e"),
+    p.add_argument("--only", choices=("cfg1", "cfg2", "cfg3", "prefill", "e2e", "floor", "valu"),
                    help="time one leg and print its JSON (for per-leg kernel profiles)")
+    p.add_argument("--trace-summary", metavar="TRACE",
+                   help="summarise a rocprofv3 kernel trace of one leg (kernel_trace.csv or "
+                        "the rocpd results.db) as Markdown and exit (no GPU); with --leg, "
+                        "--trace-steps and --trace-launches")
+    p.add_argument("--leg", default="cfg2", help="leg name for --trace-summary")
+    p.add_argument("--trace-steps", type=int, default=0,
+                   help="timed steps of the traced leg (--trace-summary)")
+    p.add_argument("--trace-launches", type=int, default=24,
+                   help="hot-path dispatches per step of the traced leg (--trace-summary)")
     p.add_argument("--pmc-sample", action="store_true",
                    help="run a short fixed kernel sequence for rocprofv3 --pmc and exit")
     p.add_argument("--traffic-from", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -79,7 +88,11 @@ class GraphStep:
 
 
 def _time_graphs(graphs, steps, warmup):
-    """Replay graphs round-robin; return ms per replay (HIP events on the replay stream)."""
+    """Replay graphs round-robin; return ms per replay (HIP events on the replay
+    stream).  The timed replays continue the warm-up's rotation, so the first
+    timed graph is the one after the last warm-up graph: with a rotation set
+    larger than the MALL, no timed replay starts on data a warm-up replay has
+    just left in the caches."""
     import torch
 
     for i in range(warmup):
@@ -88,7 +101,7 @@ def _time_graphs(graphs, steps, warmup):
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for i in range(steps):
-        graphs[i % len(graphs)].replay()
+        graphs[(warmup + i) % len(graphs)].replay()
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / steps
@@ -208,8 +221,11 @@ def bench_long_decode(steps, warmup, dev):
         return run
 
     graphs = [GraphStep(run_fn(g)) for g in range(max(1, reps // per_graph))]
-    ms = _time_graphs(graphs, max(1, steps // 8), max(1, warmup // 8)) / per_graph
-    return dict(us_per_layer=ms * 1e3, bytes=base.valid_bytes, splits=splits)
+    # At least one pass over every cache set (reps calls), in whole passes.
+    n = len(graphs) * max(1, -(-max(1, steps // 8) // len(graphs)))
+    ms = _time_graphs(graphs, n, max(1, warmup // 8)) / per_graph
+    return dict(us_per_layer=ms * 1e3, bytes=base.valid_bytes, splits=splits, calls=n * per_graph,
+                caches=reps, fused=len(flash) > 4)
 
 
 def bench_bandwidth_decode(steps, warmup, dev, batch, length):
@@ -397,6 +413,193 @@ def hbm_read_ceiling(dev, sizes_mib=(16, 256), workgroups=(512, 1024, 2048, 4096
     return out
 
 
+def launch_floor(dev, shapes=((128, 512, "config 2: 16 splits x 8 (b, kv head), 8 waves"),
+                               (256, 256, "config 3: 128 splits x 2 kv heads, 4 waves")),
+                 per_graph=24, steps=40, warmup=4):
+    """What a decode launch of a given shape cannot go under: graph-replayed
+    qf_launch_probe kernels (include/qf_probe.h) of the decode launch's grid,
+    24 nodes per graph as in a config-2 step -- an empty kernel (the cost of
+    a graph node), one dependent HBM round trip (every thread loads 16 bytes
+    of a region no earlier launch in the rotation touched) and two (a device
+    index read first, as a decode split reads kv_last before its first tile).
+    Per-launch microseconds."""
+    import torch
+
+    from qwenforge_amd import _lib
+
+    lib = _lib.load()
+    out = {}
+    pool = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
+    index = torch.zeros(1, dtype=torch.int64, device=dev)
+    for wg, threads, what in shapes:
+        region = wg * threads * 16
+        n_regions = pool.numel() // region
+        sink = torch.zeros(wg * threads // 64, dtype=torch.int32, device=dev)
+        row = {"workgroups": wg, "threads": threads, "what": what}
+        for trips, key in ((0, "empty_us"), (1, "one_round_trip_us"), (2, "two_round_trips_us")):
+            def run(g, trips=trips):
+                def body():
+                    for j in range(per_graph):
+                        r = (g * per_graph + j) % n_regions
+                        _lib.check(lib.qf_launch_probe(pool.data_ptr() + r * region, region,
+                                                       index.data_ptr(), sink.data_ptr(), wg,
+                                                       threads, trips,
+                                                       torch.cuda.current_stream().cuda_stream),
+                                   "qf_launch_probe")
+                return body
+            graphs = [GraphStep(run(g)) for g in range(max(1, n_regions // per_graph))]
+            n = len(graphs) * max(1, -(-steps // len(graphs)))
+            row[key] = round(_time_graphs(graphs, n, warmup) / per_graph * 1e3, 3)
+        out[f"{wg}x{threads}"] = row
+    del pool
+    torch.cuda.empty_cache()
+    return out
+
+
+def bench_valu_vs_mfma(steps, warmup, dev):
+    """The decode split launch as GQA-packed MFMA tiles (qf_decode_split, the
+    product) against VALU dot products (qf_decode_split_valu, a comparison
+    kernel) at the same split count, on the same caches rotated past the MALL,
+    no bias: config 1 (B=1 L=512), config 2 (B=4 ragged, kv_last per row),
+    config 3 (B=1 L=32768, 1% keys x8) and B=16 L=32768 (bandwidth regime).
+    Split kernel alone (graph-replayed), per call; both partial sets merge to
+    within 2e-3 of each other through the combine launch (tests cover the
+    oracle)."""
+    import torch
+
+    from qwenforge_amd import _lib, ops, workloads
+
+    lib = _lib.load()
+    shapes = (("config1", workloads.decode_uniform(1, 512, seed=0), 16),
+              ("config2", workloads.decode_ragged(4, seed=0), 32),
+              ("config3", workloads.decode_uniform(1, 32768, seed=0, heavy_frac=0.01), 128),
+              ("B16_L32768", workloads.decode_uniform(16, 32768, seed=1), 8))
+    out = {}
+    for name, base, splits in shapes:
+        b = base.grouped.shape[0]
+        cap = base.key_cache.shape[2]
+        per = base.key_cache.numel() * 2 * 2
+        reps = max(2, -(-2 * MALL_BYTES // per))
+        q = base.grouped.to(dev)
+        k0, v0 = base.key_cache.to(dev), base.value_cache.to(dev)
+        ks = [k0] + [k0.clone() for _ in range(reps - 1)]
+        vs = [v0] + [v0.clone() for _ in range(reps - 1)]
+        kv_last = torch.tensor([n - 1 for n in base.lengths], dtype=torch.int64, device=dev)
+        flash = ops.make_flash_scratch(b, 2, 7, cap, dev, splits=splits, fused=False)
+        acc, m, l = flash[:3]
+
+        def call(fn, r):
+            st = torch.cuda.current_stream().cuda_stream
+            common = (q.data_ptr(), *q.stride()[:3], ks[r].data_ptr(), *ks[r].stride()[:3],
+                      vs[r].data_ptr(), *vs[r].stride()[:3])
+            if fn == "mfma":
+                rc = lib.qf_decode_split(*common, None, 0, kv_last.data_ptr(), 1, acc.data_ptr(),
+                                         m.data_ptr(), l.data_ptr(), splits, b, 2, 7, 64, cap,
+                                         0.125, st)
+            else:
+                rc = lib.qf_decode_split_valu(*common, kv_last.data_ptr(), 1, acc.data_ptr(),
+                                              m.data_ptr(), l.data_ptr(), splits, b, 2, 7, 64,
+                                              cap, 0.125, st)
+            _lib.check(rc, fn)
+
+        row = {"splits": splits, "bytes": base.valid_bytes, "caches": reps}
+        outs = {}
+        for fn in ("mfma", "valu"):
+            call(fn, 0)
+            outs[fn] = ops.flash_decode_combine(flash).clone()
+            g = GraphStep(lambda fn=fn: [call(fn, r) for r in range(reps)])
+            us = _time_graphs([g], max(2, steps // 10), max(1, warmup // 10)) / reps * 1e3
+            row[f"{fn}_split_us"] = round(us, 3)
+            row[f"{fn}_GBps"] = round(base.valid_bytes / (us * 1e-6) / 1e9, 1)
+        torch.cuda.synchronize()
+        row["valu_over_mfma"] = round(row["valu_split_us"] / row["mfma_split_us"], 3)
+        row["max_abs_diff"] = float((outs["mfma"].float() - outs["valu"].float()).abs().max())
+        out[name] = row
+        del ks, vs
+        torch.cuda.empty_cache()
+    return out
+
+
+def _trace_dispatches(path):
+    """(kernel name, grid in workgroups, start ns, end ns) of every dispatch in
+    a rocprofv3 kernel trace: the CSV of ``--output-format csv`` or the rocpd
+    database rocprofv3 writes by default."""
+    out = []
+    if path.endswith(".db"):
+        import sqlite3
+
+        con = sqlite3.connect(path)
+        q = "select name, grid_x, workgroup_x, grid_y, grid_z, start, end from kernels"
+        for name, gx, wx, gy, gz, st, en in con.execute(q):
+            out.append((name, (int(gx) // max(1, int(wx)), int(gy), int(gz)), int(st), int(en)))
+        con.close()
+    else:
+        import csv
+
+        for r in csv.DictReader(open(path)):
+            grid = (int(r["Grid_Size_X"]) // max(1, int(r["Workgroup_Size_X"])),
+                    int(r["Grid_Size_Y"]), int(r["Grid_Size_Z"]))
+            out.append((r["Kernel_Name"], grid, int(r["Start_Timestamp"]),
+                        int(r["End_Timestamp"])))
+    return [(n.split("(")[0].replace("void ", "").strip(), g, st, en) for n, g, st, en in out]
+
+
+def trace_summary(path, leg, steps, launches, hot=("decode_", "prefill", "rope_kv"),
+                  gap_us=5.0):
+    """Per-kernel and per-step figures of one bench leg from a rocprofv3
+    kernel trace (``--kernel-trace``), as Markdown.
+
+    The leg's hot-path dispatches (kernel names containing one of ``hot``)
+    are cut into replays wherever one starts more than ``gap_us`` after the
+    previous one ends; the timed region is the last ``steps`` replays of
+    exactly ``launches`` dispatches (the eager warm-up calls and the earlier
+    replays come before it).  Reported over the timed region: per kernel the
+    dispatch count and mean / median duration; per replay the span (first
+    start to last end) and that span per launch, the trace's counterpart of
+    the bench's HIP-event time per launch (which also holds the gaps between
+    replays, where the profiler slows the host's graph submission)."""
+    ds = sorted(_trace_dispatches(path), key=lambda d: d[2])
+    lines = [f"Kernel trace `{os.path.basename(path)}`, leg `{leg}`.", ""]
+    hot_d = [d for d in ds if any(h in d[0] for h in hot)]
+    groups, cur = [], []
+    for d in hot_d:
+        if cur and (d[2] - cur[-1][3]) / 1e3 > gap_us:
+            groups.append(cur)
+            cur = []
+        cur.append(d)
+    if cur:
+        groups.append(cur)
+    full = [g for g in groups if len(g) == launches]
+    timed = full[-steps:] if steps > 0 else full
+    lines.append(f"{len(hot_d)} hot-path dispatches in {len(groups)} bursts; {len(full)} bursts of "
+                 f"exactly {launches} (one replay); the timed region is the last {len(timed)}.")
+    if timed:
+        per = {}
+        for g in timed:
+            for name, grid, st, en in g:
+                per.setdefault((name, grid), []).append((en - st) / 1e3)
+        lines += ["", "| kernel (timed region) | grid (workgroups) | dispatches | mean µs | "
+                      "median µs |", "|---|---|---:|---:|---:|"]
+        for (name, grid), durs in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+            lines.append(f"| `{name}` | {grid[0]}x{grid[1]}x{grid[2]} | {len(durs)} | "
+                         f"{statistics.mean(durs):.3f} | {statistics.median(durs):.3f} |")
+        spans = [(max(d[3] for d in g) - g[0][2]) / 1e3 for g in timed]
+        busy = [sum(d[3] - d[2] for d in g) / 1e3 for g in timed]
+        lines += ["", "| per replay (timed region) | µs |", "|---|---:|",
+                  f"| span, median (first start to last end) | {statistics.median(spans):.3f} |",
+                  f"| span / {launches} launches | {statistics.median(spans) / launches:.3f} |",
+                  f"| sum of kernel durations, median | {statistics.median(busy):.3f} |"]
+    alln = {}
+    for name, grid, st, en in ds:
+        alln.setdefault((name, grid), []).append((en - st) / 1e3)
+    lines += ["", "| kernel (whole run) | grid (workgroups) | dispatches | mean µs | median µs |",
+              "|---|---|---:|---:|---:|"]
+    for (name, grid), durs in sorted(alln.items(), key=lambda kv: -sum(kv[1]))[:25]:
+        lines.append(f"| `{name}` | {grid[0]}x{grid[1]}x{grid[2]} | {len(durs)} | "
+                     f"{statistics.mean(durs):.3f} | {statistics.median(durs):.3f} |")
+    return "\n".join(lines)
+
+
 def bench_prefill(steps, warmup, dev, seq=2048):
     """Config 4: causal prefill S=2048 with fused RoPE + cache append (other
     lengths for the long-prompt leg)."""
@@ -581,14 +784,27 @@ def _traffic(kernel):
 
 
 def _cpu_model():
+    """The host CPU as /proc/cpuinfo names it: model name plus family / model /
+    stepping (a virtualised host may report a generic model name)."""
+    info = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if ":" not in line:
+                    if info:
+                        break
+                    continue
+                k, v = (x.strip() for x in line.split(":", 1))
+                if k in ("vendor_id", "model name", "cpu family", "model", "stepping",
+                         "cpu MHz", "cache size") and k not in info:
+                    info[k] = v
     except OSError:
-        pass
-    return "unknown"
+        return "unknown"
+    name = info.get("model name", "unknown")
+    return (f"{name} (vendor {info.get('vendor_id', '?')}, family {info.get('cpu family', '?')}, "
+            f"model {info.get('model', '?')}, stepping {info.get('stepping', '?')}, "
+            f"{info.get('cpu MHz', '?')} MHz, cache {info.get('cache size', '?')}, "
+            f"{os.cpu_count()} logical CPUs)")
 
 
 def _time_oracle(layers, seconds, threads, form="fp32"):
@@ -630,7 +846,7 @@ def _cpu_row(layers, seconds, threads, form, what):
     }
 
 
-def _cpu_decode_step(threads, reps=5):
+def _cpu_decode_step(threads, reps=20, warm=3):
     """Config 5 on the CPU: the fp32 oracle's decode step (SE:876-982,
     oracle.model.decode_step) of the full Qwen2.5-0.5B shape at B=1 and B=4
     over 1152-slot caches with 1024 valid slots.  The cache holds random
@@ -656,24 +872,76 @@ def _cpu_decode_step(threads, reps=5):
                    torch.randn(b, 2, 1152, 64, generator=gen)) for _ in range(cfg.layers)]
         state[b] = (caches, torch.randint(0, cfg.vocab, (b,), generator=gen))
     # Warm-up steps at both batch sizes first (thread pool, first touch of the
-    # fp32 weights), then the timed steps, alternating the batch sizes.
-    for b in (1, 4, 1, 4):
-        caches, tok = state[b]
-        om.decode_step(w, cfg, tok, torch.full((b,), 1024), caches, 1024)
+    # fp32 weights), then the timed steps, alternating the batch sizes.  The
+    # steps write cache slots 1024 .. 1024 + warm + reps - 1 (< 1152).
+    for i in range(warm):
+        for b in (1, 4):
+            caches, tok = state[b]
+            om.decode_step(w, cfg, tok, torch.full((b,), 1024 + i), caches, 1024 + i)
     times = {1: [], 4: []}
     for i in range(reps):
         for b in (1, 4):
             caches, tok = state[b]
+            p = 1024 + warm + i
             t0 = time.perf_counter()
-            om.decode_step(w, cfg, tok, torch.full((b,), 1025 + i), caches, 1025 + i)
+            om.decode_step(w, cfg, tok, torch.full((b,), p), caches, p)
             times[b].append(time.perf_counter() - t0)
     for b in (1, 4):
         med = statistics.median(times[b])
         out[f"tok_s_bs{b}"] = round(b / med, 2)
         out[f"ms_per_step_bs{b}"] = round(med * 1e3, 1)
-    out["sample"] = (f"median of {reps} timed steps per batch (after two warm-up steps at each), "
-                     "fp32 oracle decode step, 24 layers + lm_head, 1024 valid cache slots")
+    out["threads"] = threads
+    out["sample"] = (f"median of {reps} timed steps per batch after {warm} warm-up steps at each, "
+                     "fp32 oracle decode step, 24 layers + lm_head, 1024+ valid cache slots")
     return out
+
+
+def _cpu_prefill(threads, reps, warm, seq=2048):
+    """Config 4 on the CPU (RoPE theta=1e6 + causal prefill + cache append,
+    B=1, S=2048, 14q/2kv, hd64), in the fp32 oracle form (oracle.apply_rope_fp16
+    + oracle.causal_prefill + oracle.append_prefill) and in the reference's
+    own fp16 eager form (the same RoPE and append around
+    oracle.eager_attention_fp16, SE:579-599).  Median of `reps` calls after
+    `warm` warm-ups, at `threads` threads."""
+    import torch
+
+    import oracle
+    from qwenforge_amd import workloads
+
+    torch.set_num_threads(threads)
+    case = workloads.prefill_case(seq, seed=0)
+    kc = torch.zeros(1, 2, seq, 64, dtype=torch.float16)
+    vc = torch.zeros_like(kc)
+
+    def fp32():
+        q = oracle.apply_rope_fp16(case.query, case.cos, case.sin)
+        k = oracle.apply_rope_fp16(case.key, case.cos, case.sin)
+        oracle.append_prefill(kc, vc, k, case.value)
+        return oracle.causal_prefill(q, k, case.value)
+
+    def fp16():
+        q = oracle.apply_rope_fp16(case.query, case.cos, case.sin)
+        k = oracle.apply_rope_fp16(case.key, case.cos, case.sin)
+        oracle.append_prefill(kc, vc, k, case.value)
+        return oracle.eager_attention_fp16(q, k, case.value)
+
+    out = {}
+    for name, fn in (("fp32_oracle", fp32), ("fp16_reference_form", fp16)):
+        for _ in range(warm):
+            fn()
+        times = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        med = statistics.median(times)
+        out[name] = {"us_per_call": round(med * 1e6, 1),
+                     "TFLOPs": round(case.flops / med / 1e12, 4),
+                     "sample": f"median of {reps} calls after {warm} warm-ups, "
+                               f"{sum(times):.1f} s timed"}
+    out["threads"] = threads
+    return out
+
 
 
 def cpu_baseline(layers, seconds):
@@ -687,10 +955,15 @@ def cpu_baseline(layers, seconds):
     threads = len(os.sched_getaffinity(0))
     share = seconds / 4
     cfg1 = [workloads.decode_uniform(1, 512, seed=i) for i in range(8)]
+    cfg3 = [workloads.decode_uniform(1, 32768, seed=i, heavy_frac=0.01) for i in range(2)]
     c2_32 = _cpu_row(layers, share * 1.6, threads, "fp32", "config-2")
     c2_16 = _cpu_row(layers, share * 0.8, threads, "fp16", "config-2")
     c1_32 = _cpu_row(cfg1, share * 0.8, threads, "fp32", "config-1")
     c1_16 = _cpu_row(cfg1, share * 0.8, threads, "fp16", "config-1")
+    c3_32 = _cpu_row(cfg3, share * 0.4, threads, "fp32", "config-3")
+    c3_16 = _cpu_row(cfg3, share * 0.4, threads, "fp16", "config-3")
+    c4 = _cpu_prefill(threads, reps=20, warm=3)
+    c4_1 = _cpu_prefill(1, reps=3, warm=1)
     return {
         "value": c2_32["GBps"],
         "unit": "GB/s",
@@ -702,6 +975,12 @@ def cpu_baseline(layers, seconds):
         "config2": {"fp32_oracle": c2_32, "fp16_reference_form": c2_16},
         "config1": {"fp32_oracle": c1_32, "fp16_reference_form": c1_16,
                     "what": "B=1, L=512, 14q/2kv, hd64, one layer (265,728 B)"},
+        "config3": {"fp32_oracle": c3_32, "fp16_reference_form": c3_16,
+                    "what": "B=1, L=32768, 1% of keys x8, 14q/2kv, hd64, one layer "
+                            "(16,780,800 B); two distinct caches"},
+        "config4": {**c4, "single_thread": c4_1,
+                    "what": "B=1, S=2048 prefill: RoPE (theta 1e6) + causal attention + cache "
+                            "append, 7,519,862,784 FLOP per call"},
         "config5": _cpu_decode_step(threads),
         "cpu_model": _cpu_model(),
     }
@@ -718,6 +997,10 @@ def _only(leg, steps, warmup, dev):
                                 "splits": r["splits"], "fused": r["fused"]}}
     if leg == "cfg3":
         return {"long_decode_cfg3": bench_long_decode(steps, warmup, dev)}
+    if leg == "floor":
+        return {"launch_floor": launch_floor(dev)}
+    if leg == "valu":
+        return {"valu_vs_mfma": bench_valu_vs_mfma(steps, warmup, dev)}
     if leg == "prefill":
         pf = bench_prefill(steps, warmup, dev)
         return {"prefill_cfg4": {"us_per_layer": pf["us_per_layer"],
@@ -730,6 +1013,9 @@ def main():
     args = _args()
     if args.traffic_from:
         traffic_summary(*args.traffic_from)
+        return
+    if args.trace_summary:
+        print(trace_summary(args.trace_summary, args.leg, args.trace_steps, args.trace_launches))
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -809,6 +1095,15 @@ def main():
             "merge": "fused single launch" if r["fused"] else "split + combine launches",
         },
     }
+    floor = launch_floor(dev)
+    f2 = floor["128x512"]
+    line["roofline"]["launch_floor_us"] = {
+        "empty": f2["empty_us"], "one_round_trip": f2["one_round_trip_us"],
+        "two_round_trips": f2["two_round_trips_us"],
+        "what": "graph-replayed qf_launch_probe kernels of this launch's grid (128 workgroups x "
+                "512 threads), 24 per graph: an empty node, one dependent HBM round trip, two "
+                "(a device index, then the tile, as kv_last then the first K/V tile)"}
+    line["launch_floor"] = floor
     if not args.no_extras:
         c1 = bench_decode_cfg1(args.steps, args.warmup, dev)
         line["decode_cfg1"] = {
@@ -828,6 +1123,9 @@ def main():
             "GBps": round(lg["bytes"] / (lg["us_per_layer"] * 1e-6) / 1e9, 1),
             "hbm_frac": round(lg["bytes"] / (lg["us_per_layer"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "splits": lg["splits"],
+            "merge": "fused single launch" if lg["fused"] else "split + combine launches",
+            "timed_calls": lg["calls"],
+            "caches": lg["caches"],
         }
         bw = {}
         for b, L in ((12, 5760), (16, 32768), (64, 4096)):

@@ -14,9 +14,10 @@ make the restatement trustworthy live in ``tests/test_oracle_*.py``:
   library routine), against fp64 brute-force loops, and against the
   reference's whiteboard known-answer logits (causal attention + split-half
   RoPE).
-* ``grouped_decode_attention_fp16`` (the reference's fp16 form, timed as a
-  CPU baseline only): within fp16 rounding of fp64 SDPA, exact on uniform V
-  and on a single valid key, fp16 output.
+* ``grouped_decode_attention_fp16`` and ``eager_attention_fp16`` (the
+  reference's fp16 forms, timed as CPU baselines only): within fp16 rounding
+  of fp64 SDPA, exact on uniform V (and, causal, on the first query row,
+  which sees only key 0), fp16 output.
 * ``split_partials`` / ``combine_partials``: invariants (independence of the
   split count, S=1 equals the unsplit path, empty and fully masked splits,
   single valid key, uniform V, key permutation).
@@ -41,6 +42,7 @@ from .attention import (  # noqa: F401
     causal_prefill,
     combine_partials,
     eager_attention,
+    eager_attention_fp16,
     flash_decode,
     grouped_decode_attention,
     grouped_decode_attention_fp16,

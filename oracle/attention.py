@@ -50,6 +50,30 @@ def eager_attention(
     return torch.matmul(probs, v)
 
 
+def eager_attention_fp16(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    causal: bool = True,
+) -> torch.Tensor:
+    """The reference's own fp16 form of ``_eager_attention`` (SE:579-599), for
+    the CPU baseline of the prefill: K/V heads repeated G times, fp16 scores
+    ``Q @ K^T * D**-0.5``, the bottom-right causal mask filled with the fp16
+    minimum, ``softmax(scores.float())`` rounded to fp16, then fp16
+    ``probabilities @ V``.  Returns fp16 (B, QH, Lq, D).
+    """
+    groups = query.shape[1] // key.shape[1]
+    k = key.repeat_interleave(groups, dim=1)
+    v = value.repeat_interleave(groups, dim=1)
+    scores = torch.matmul(query, k.transpose(-2, -1)) * (query.shape[-1] ** -0.5)
+    if causal:
+        lq, lk = scores.shape[-2:]
+        keep = torch.ones((lq, lk), dtype=torch.bool).tril(diagonal=lk - lq)
+        scores = scores.masked_fill(~keep, torch.finfo(scores.dtype).min)
+    probabilities = torch.softmax(scores.float(), dim=-1).to(query.dtype)
+    return torch.matmul(probabilities, v)
+
+
 def grouped_decode_attention(
     grouped: torch.Tensor,
     key_cache: torch.Tensor,

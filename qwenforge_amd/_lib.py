@@ -214,6 +214,17 @@ SIGNATURES = {
     ],
     # include/qf_probe.h
     "qf_stream_read": [_vp, _i64, _vp, _i32, _vp],   # src, bytes, sink, workgroups, stream
+    "qf_launch_probe": [_vp, _i64, _vp, _vp,          # src, bytes, index, sink
+                        _i32, _i32, _i32, _vp],      # workgroups, threads, round_trips, stream
+    "qf_decode_split_valu": [
+        _vp, _i64, _i64, _i64,          # q
+        _vp, _i64, _i64, _i64,          # k
+        _vp, _i64, _i64, _i64,          # v
+        _vp, _i64,                      # kv_last, kv_last_sb
+        _vp, _vp, _vp, _i32,            # acc, m, l, splits
+        _i32, _i32, _i32, _i32, _i32,   # B, KVH, G, D, cap
+        _f32, _vp,                      # scale, stream
+    ],
     "qf_error_string": [_i32],
     "qf_abi_version": [],
 }

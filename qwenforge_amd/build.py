@@ -23,7 +23,7 @@ LIB_PATH = PKG / "_qf_attn.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 SOURCES = ["decode_attn.hip", "prefill_attn.hip", "rope_append.hip", "decode_step.hip", "probe.hip",
-           "capi.cpp"]
+           "decode_valu.hip", "capi.cpp"]
 # Packed-fp32 VALU forms are disabled for all device code (they have produced
 # silently wrong results on this hardware pool); hipcc's host pass warns that it
 # does not know the feature, which is harmless.

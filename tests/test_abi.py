@@ -101,6 +101,17 @@ def test_stream_read_rejects_bad_arguments():
     assert lib.qf_stream_read(16, 1024, 16, 0, None) == -1
 
 
+def test_launch_probe_rejects_bad_arguments():
+    lib = _lib.load()
+    assert lib.qf_launch_probe(16, 1024, 16, 16, 4, 100, 1, None) == -1   # threads not x64
+    assert lib.qf_launch_probe(16, 1024, 16, 16, 4, 2048, 1, None) == -1  # > 1024 threads
+    assert lib.qf_launch_probe(16, 1024, 16, 16, 0, 256, 1, None) == -1   # no workgroups
+    assert lib.qf_launch_probe(16, 1024, 16, 16, 4, 256, 3, None) == -1   # round trips > 2
+    assert lib.qf_launch_probe(None, 1024, 16, 16, 4, 256, 1, None) == -1  # no source
+    assert lib.qf_launch_probe(16, 1000, 16, 16, 4, 256, 1, None) == -1   # bytes not x16
+    assert lib.qf_launch_probe(16, 1024, None, 16, 4, 256, 2, None) == -1  # no index
+
+
 def test_noalloc_decode_rejects_before_any_hip_call():
     """Shape, size and pointer checks of qf_decode_attn_noalloc return before the
     library touches the device (no GPU here)."""

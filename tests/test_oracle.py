@@ -129,6 +129,33 @@ def test_grouped_decode_fp16_form_within_fp16_rounding_of_sdpa():
                        v[:, :, 17:18].expand(b, kvh, g, 64))
 
 
+def test_eager_prefill_fp16_form_within_fp16_rounding_of_sdpa():
+    """The reference's fp16 eager prefill (SE:579-599): against fp64 causal
+    SDPA with K/V repeated it is off by fp16 rounding only; the first query
+    row equals V[0] of its kv head exactly and uniform V is reproduced
+    exactly; a dropped causal mask or a transposed head mapping fails."""
+    gen = torch.Generator().manual_seed(32)
+    s = 96
+    q = _rand(gen, 1, 14, s, 64)
+    k = _rand(gen, 1, 2, s, 64)
+    v = _rand(gen, 1, 2, s, 64)
+    got = oracle.eager_attention_fp16(q, k, v)
+    assert got.dtype == torch.float16
+    ref = F.scaled_dot_product_attention(q.double(), k.double().repeat_interleave(7, 1),
+                                         v.double().repeat_interleave(7, 1), is_causal=True)
+    err = (got.double() - ref).abs().max().item()
+    assert 0 < err < 4e-3, err
+    assert torch.equal(got[:, :, 0], v[:, :, 0].repeat_interleave(7, 1))
+    row = _rand(gen, 64)
+    uni = row.expand(1, 2, s, 64).contiguous()
+    assert torch.equal(oracle.eager_attention_fp16(q, k, uni), row.expand(1, 14, s, 64))
+    no_mask = oracle.eager_attention_fp16(q, k, v, causal=False)
+    assert (no_mask.double() - ref).abs().max().item() > 0.1
+    swapped = F.scaled_dot_product_attention(q.double(), k.double().repeat(1, 7, 1, 1),
+                                             v.double().repeat(1, 7, 1, 1), is_causal=True)
+    assert (got.double() - swapped).abs().max().item() > 0.1
+
+
 def test_grouped_decode_head_mapping_is_h_div_g():
     """Query head h of the flattened (B, 14) layout must read kv head h // 7."""
     gen = torch.Generator().manual_seed(3)
