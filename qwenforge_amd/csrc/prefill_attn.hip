@@ -513,8 +513,8 @@ __device__ __forceinline__ void lds_issue(LdsCtx& c, unsigned char* Kd, unsigned
   c.vrem -= vstep;
 }
 
-// v_max3_f32 on raw registers.  fmaxf would first canonicalise every MFMA
-// result (v_max_f32 x, x per operand: IEEE mode quiets signalling NaNs); the
+// v_max3_f32 on raw registers.  fmaxf would first canonicalise the MFMA
+// results (v_max_f32 x, x per operand: IEEE mode quiets signalling NaNs); the
 // scores here are finite or -inf, so the plain three-input max is exact.
 __device__ __forceinline__ float max3_raw(float a, float b, float c) {
   float r;
@@ -522,8 +522,14 @@ __device__ __forceinline__ float max3_raw(float a, float b, float c) {
   return r;
 }
 
-// Max of a lane's 16 scores: a depth-3 tree of seven max3.
-__device__ __forceinline__ float max16(const f32x4 (&sc)[4]) {
+// Max of a lane's 16 scores: a depth-3 tree of seven max3.  The hazard
+// recognizer does not look into inline asm, so it would insert no wait
+// states between the score MFMAs and an asm read of their results: the
+// s_nops, tied to all sixteen score registers (every max3 depends on them,
+// and they on the MFMAs), give a matrix-core result the 16 wait states it
+// may need before a VALU read, however close the scheduler puts the max.
+__device__ __forceinline__ float max16(f32x4 (&sc)[4]) {
+  asm volatile("s_nop 7\n\ts_nop 7" : "+v"(sc[0]), "+v"(sc[1]), "+v"(sc[2]), "+v"(sc[3]));
   const float a = max3_raw(sc[0][0], sc[0][1], sc[0][2]);
   const float b = max3_raw(sc[0][3], sc[1][0], sc[1][1]);
   const float d = max3_raw(sc[1][2], sc[1][3], sc[2][0]);
