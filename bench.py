@@ -107,6 +107,25 @@ def _time_graphs(graphs, steps, warmup):
     return start.elapsed_time(end) / steps
 
 
+def _replay_spans(graphs, n, first):
+    """Median GPU time inside one graph replay, ms: each of `n` replays
+    (continuing the rotation at graph `first`) is bracketed by HIP events on
+    the replay stream, so the figure excludes the gap between one replay's
+    last node and the next replay's first (the per-graph launch cost, which
+    ``_time_graphs`` includes) -- the counterpart of a kernel trace's span
+    from a replay's first dispatch start to its last dispatch end."""
+    import torch
+
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(n)]
+    for i in range(n):
+        ev[i][0].record()
+        graphs[(first + i) % len(graphs)].replay()
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    return statistics.median(a.elapsed_time(b) for a, b in ev)
+
+
 def bench_ragged_decode(steps, warmup, dev):
     """Config 2: 24 per-layer decode-attention launches per step."""
     import torch
@@ -135,6 +154,7 @@ def bench_ragged_decode(steps, warmup, dev):
 
     graphs = [GraphStep(step_fn(cs)) for cs in sets]
     ms = _time_graphs(graphs, steps, warmup)
+    ms_span = _replay_spans(graphs, max(len(graphs), steps), warmup + steps)
     step_bytes = sum(c.valid_bytes for c in layers)
     fused = len(flash) > 4
 
@@ -156,7 +176,7 @@ def bench_ragged_decode(steps, warmup, dev):
         ms_combine = _time_graphs([comb], steps, warmup)
     return dict(ms_per_step=ms, step_bytes=step_bytes, launches=len(layers), splits=splits,
                 replicas=replicas, layers=layers, fused=fused, ms_split=ms_split,
-                ms_combine=ms_combine)
+                ms_combine=ms_combine, ms_span=ms_span)
 
 
 def bench_decode_cfg1(steps, warmup, dev):
@@ -994,6 +1014,7 @@ def _only(leg, steps, warmup, dev):
     if leg == "cfg2":
         r = bench_ragged_decode(steps, warmup, dev)
         return {"decode_cfg2": {"us_per_layer": r["ms_per_step"] * 1e3 / r["launches"],
+                                "us_per_launch_in_replay": r["ms_span"] * 1e3 / r["launches"],
                                 "splits": r["splits"], "fused": r["fused"]}}
     if leg == "cfg3":
         return {"long_decode_cfg3": bench_long_decode(steps, warmup, dev)}
@@ -1052,7 +1073,10 @@ def main():
     gbs = r["step_bytes"] / (ms * 1e-3) / 1e9
     us_layer = ms * 1e3 / r["launches"]
     launch_bytes = r["step_bytes"] / r["launches"]
-    us_split = r["ms_split"] * 1e3 / r["launches"]
+    # The roofline's per-launch time: the replay's own span (first node start
+    # to last node end, HIP events around each replay) over its launches; with
+    # split + combine launches, the split launch alone.
+    us_split = (r["ms_span"] if r["fused"] else r["ms_split"]) * 1e3 / r["launches"]
     split_gbs = launch_bytes / (us_split * 1e-6) / 1e9
     line = {
         "metric": "flash-decode µs/layer + HBM GB/s (% of peak); decode tok/s at bs=1/4",
@@ -1090,6 +1114,10 @@ def main():
                             if r["fused"] else "qf_decode_split: the split launch (partial mode)"),
             "bytes_per_launch": int(launch_bytes),
             "avg_launch_us": round(us_split, 3),
+            "avg_launch_us_what": ("median span of one graph replay (HIP events right before and "
+                                   "after each replay) / 24 launches; ms_per_step also holds the "
+                                   "gap between replays"),
+            "replay_gap_us": round((ms - r["ms_span"]) * 1e3, 3),
             "combine_kernel_avg_us": (None if r["ms_combine"] is None
                                       else round(r["ms_combine"] * 1e3 / r["launches"], 3)),
             "merge": "fused single launch" if r["fused"] else "split + combine launches",
