@@ -34,6 +34,8 @@
 // rescaled when the running max grows by more than kRescaleSlack); Q is
 // rotated in registers once at the start.  The causal mask is applied only on
 // the diagonal and tail tiles.
+#include <atomic>
+
 #include "qf_common.h"
 #include "../../include/qf_attn.h"
 #include "../../include/qf_paged.h"
@@ -68,6 +70,11 @@ struct Args {
   int64_t o_sb, o_sh, o_sn;
   int B, QH, KVH, G, S;
   float scale_log2;
+  // Work order of the streaming kernel's one-dimensional grid: workgroups
+  // [0, snake) take items 0.. (heaviest query tiles first), workgroups from
+  // `snake` on take the remaining items lightest first; 0: heaviest first
+  // throughout.
+  int snake;
   // Packed variable-length rows (ragged prefill): row b's tokens are
   // [cu[b], cu[b+1]) of q/k/v/out/cos/sin, whose batch strides are then 0;
   // S holds the longest row.  kv_packed: k/v are those packed inputs (1) or
@@ -664,8 +671,12 @@ __global__ __launch_bounds__(kG * 4 * 64, 4) void prefill_lds2_kernel(Args a) {
   // fastest and the heaviest query tiles first.
   const int n_bq = a.B * a.QH;
   const int n_mtiles = (a.S + kBM - 1) / kBM;
-  const int mt = n_mtiles - 1 - (int)(blockIdx.x / n_bq);
-  const int bq = (int)(blockIdx.x % n_bq);
+  // Item (query tile, head) of this workgroup, in heaviest-first order; the
+  // second round of workgroups (a second one per CU) runs the order backwards.
+  int item = (int)blockIdx.x;
+  if (a.snake > 0 && item >= a.snake) item = (int)gridDim.x - 1 - (item - a.snake);
+  const int mt = n_mtiles - 1 - item / n_bq;
+  const int bq = item % n_bq;
   const int b = bq / a.QH, hq = bq % a.QH;
   const int hk = hq / a.G;
   const int tid = threadIdx.x;
@@ -880,6 +891,29 @@ using qf::prefill::Args;
 
 // Shared launch sequence of the dense and the packed (varlen) entry points;
 // `a` is filled and validated.  Returns 0 or a QF_ERR_* / hipError_t code.
+// CUs of the device that owns `st` (cached per device); 0 if it cannot be read.
+static int stream_cus(hipStream_t st) {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cached[kMaxDevices];
+  int dev = -1;
+  if (st == nullptr) {
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+  } else {
+    hipDevice_t d = -1;
+    if (hipStreamGetDevice(st, &d) != hipSuccess) return 0;
+    dev = (int)d;
+  }
+  if (dev < 0 || dev >= kMaxDevices) return 0;
+  int cus = cached[dev].load(std::memory_order_relaxed);
+  if (cus == 0) {
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus < 0)
+      return 0;
+    cached[dev].store(cus, std::memory_order_relaxed);
+  }
+  return cus;
+}
+
 static int prefill_launch(Args a, bool rope, bool append, hipStream_t st) {
   using namespace qf::prefill;
   const int B = a.B, QH = a.QH, KVH = a.KVH, S = a.S;
@@ -918,6 +952,17 @@ static int prefill_launch(Args a, bool rope, bool append, hipStream_t st) {
   // were slower at every size, 28.8 vs 26.0 us at S=2048).
   constexpr int G = 2;
   const dim3 lblock(G * 4 * 64);
+  // Two workgroups fit a CU.  When the grid needs more than one per CU but
+  // no more than two, the first round (one per CU, heaviest query tiles)
+  // shares each CU with a second-round workgroup; running the second round
+  // lightest first pairs the heaviest tiles with the lightest, whose short
+  // lives slow the critical ones least (measured on MI355X, same outputs:
+  // S=2048 call 23.4 -> 22.9 us, S=1536 18.8 -> 18.6, S=2304 26.1 -> 25.45).
+  a.snake = 0;
+  {
+    const int cus = stream_cus(st);
+    if (cus > 0 && lgrid.x > (unsigned)cus && lgrid.x <= 2u * (unsigned)cus) a.snake = cus;
+  }
   if (paged) {
     if (rope) hipLaunchKernelGGL((prefill_lds2_kernel<G, true, true>), lgrid, lblock, 0, st, a);
     else hipLaunchKernelGGL((prefill_lds2_kernel<G, false, true>), lgrid, lblock, 0, st, a);
