@@ -267,8 +267,10 @@ def bench_long_decode(steps, warmup, dev):
         return run
 
     graphs = [GraphStep(run_fn(g)) for g in range(max(1, reps // per_graph))]
-    # At least one pass over every cache set (reps calls), in whole passes.
-    n = len(graphs) * max(1, -(-max(1, steps // 8) // len(graphs)))
+    # Whole passes over every cache set (reps calls), at least 16 replays: the
+    # first replay's launch latency is inside the timed region, and over few
+    # replays it shows (config 3 at 4 replays read 10.09 us against 9.6).
+    n = len(graphs) * max(1, -(-max(16, steps // 8) // len(graphs)))
     ms = _time_graphs(graphs, n, max(1, warmup // 8)) / per_graph
     return dict(us_per_layer=ms * 1e3, bytes=base.valid_bytes, splits=splits, calls=n * per_graph,
                 caches=reps, fused=len(flash) > 4)
@@ -301,8 +303,8 @@ def bench_bandwidth_decode(steps, warmup, dev, batch, length):
         for r in range(reps):
             ops.flash_decode_split(q, ks[r], vs[r], None, flash[:4])
 
-    ms_full = _time_graphs([GraphStep(full)], max(1, steps // 4), max(1, warmup // 4)) / reps
-    ms_split = _time_graphs([GraphStep(split_only)], max(1, steps // 4), max(1, warmup // 4)) / reps
+    ms_full = _time_graphs([GraphStep(full)], max(16, steps // 4), max(1, warmup // 4)) / reps
+    ms_split = _time_graphs([GraphStep(split_only)], max(16, steps // 4), max(1, warmup // 4)) / reps
     nbytes = base.valid_bytes
     return dict(batch=batch, length=length, splits=splits, fused=len(flash) > 4,
                 us_full=ms_full * 1e3, us_split=ms_split * 1e3, bytes=nbytes)
@@ -351,8 +353,8 @@ def bench_paged_decode(steps, warmup, dev, batch, length, page=64):
         for r in range(reps):
             paged.flash_decode_split_paged(q, kp[r], vp[r], table, None, flash[:4])
 
-    ms_full = _time_graphs([GraphStep(full)], max(1, steps // 4), max(1, warmup // 4)) / reps
-    ms_split = _time_graphs([GraphStep(split_only)], max(1, steps // 4), max(1, warmup // 4)) / reps
+    ms_full = _time_graphs([GraphStep(full)], max(16, steps // 4), max(1, warmup // 4)) / reps
+    ms_split = _time_graphs([GraphStep(split_only)], max(16, steps // 4), max(1, warmup // 4)) / reps
     return dict(batch=batch, length=length, splits=splits, page=page,
                 us_full=ms_full * 1e3, us_split=ms_split * 1e3, bytes=base.valid_bytes)
 
@@ -554,7 +556,7 @@ def bench_valu_vs_mfma(steps, warmup, dev):
             call(fn, 0)
             outs[fn] = ops.flash_decode_combine(flash).clone()
             g = GraphStep(lambda fn=fn: [call(fn, r) for r in range(reps)])
-            us = _time_graphs([g], max(2, steps // 10), max(1, warmup // 10)) / reps * 1e3
+            us = _time_graphs([g], max(16, steps // 10), max(1, warmup // 10)) / reps * 1e3
             row[f"{fn}_split_us"] = round(us, 3)
             row[f"{fn}_GBps"] = round(base.valid_bytes / (us * 1e-6) / 1e9, 1)
         torch.cuda.synchronize()
