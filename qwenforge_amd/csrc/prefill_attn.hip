@@ -70,10 +70,9 @@ struct Args {
   int64_t o_sb, o_sh, o_sn;
   int B, QH, KVH, G, S;
   float scale_log2;
-  // Work order of the streaming kernel's one-dimensional grid: workgroups
-  // [0, snake) take items 0.. (heaviest query tiles first), workgroups from
-  // `snake` on take the remaining items lightest first; 0: heaviest first
-  // throughout.
+  // Work order of the streaming kernel's one-dimensional grid when it needs
+  // one to two workgroups per CU: the CU count (the first round), else 0
+  // (heaviest query tiles first throughout).
   int snake;
   // Packed variable-length rows (ragged prefill): row b's tokens are
   // [cu[b], cu[b+1]) of q/k/v/out/cos/sin, whose batch strides are then 0;
@@ -671,10 +670,18 @@ __global__ __launch_bounds__(kG * 4 * 64, 4) void prefill_lds2_kernel(Args a) {
   // fastest and the heaviest query tiles first.
   const int n_bq = a.B * a.QH;
   const int n_mtiles = (a.S + kBM - 1) / kBM;
-  // Item (query tile, head) of this workgroup, in heaviest-first order; the
-  // second round of workgroups (a second one per CU) runs the order backwards.
+  // Item (query tile, head) of this workgroup; items are numbered heaviest
+  // first.  With a second round (a.snake = CUs, P = grid - CUs workgroups past
+  // one per CU): the first round's last CUs - P workgroups, whose CUs get no
+  // second one, take the heaviest items; its first P take the next ones; the
+  // second round takes the rest lightest first, so workgroup CUs + j meets
+  // the item of workgroup j on its CU.
   int item = (int)blockIdx.x;
-  if (a.snake > 0 && item >= a.snake) item = (int)gridDim.x - 1 - (item - a.snake);
+  if (a.snake > 0) {
+    const int T = (int)gridDim.x, P = T - a.snake, H = a.snake - P;
+    if (item >= a.snake) item = T - 1 - (item - a.snake);
+    else item = item < P ? H + item : item - P;
+  }
   const int mt = n_mtiles - 1 - item / n_bq;
   const int bq = item % n_bq;
   const int b = bq / a.QH, hq = bq % a.QH;
@@ -953,11 +960,13 @@ static int prefill_launch(Args a, bool rope, bool append, hipStream_t st) {
   constexpr int G = 2;
   const dim3 lblock(G * 4 * 64);
   // Two workgroups fit a CU.  When the grid needs more than one per CU but
-  // no more than two, the first round (one per CU, heaviest query tiles)
-  // shares each CU with a second-round workgroup; running the second round
-  // lightest first pairs the heaviest tiles with the lightest, whose short
-  // lives slow the critical ones least (measured on MI355X, same outputs:
-  // S=2048 call 23.4 -> 22.9 us, S=1536 18.8 -> 18.6, S=2304 26.1 -> 25.45).
+  // no more than two, the first round (one per CU) shares most CUs with a
+  // second-round workgroup.  The heaviest query tiles go to the CUs that get
+  // none, the next ones are paired with the lightest (the second round runs
+  // lightest first), whose short lives slow the long ones least.  Measured on
+  // MI355X, same outputs, against heaviest-first throughout: S=2048 call 23.4
+  // -> 22.9 us, S=1536 18.8 -> 18.6, S=2304 26.1 -> 25.45 with the pairing;
+  // the unpaired heaviest tiles take about 0.1 us more off the attention.
   a.snake = 0;
   {
     const int cus = stream_cus(st);
