@@ -803,12 +803,15 @@ def traffic_summary(fetch_csv, write_csv):
 
 
 def _kernel_source_hash():
-    """sha256 prefix of the decode kernel's source (decode_attn.hip + qf_common.h)."""
+    """sha256 prefix of the decode kernel's source and build: decode_attn.hip,
+    decode_attn_fused_vec.hip (the headline instances' unit), qf_common.h and
+    build.py (which holds that unit's compiler flags)."""
     import hashlib
 
     h = hashlib.sha256()
-    for name in ("decode_attn.hip", "qf_common.h"):
-        with open(os.path.join(ROOT, "qwenforge_amd", "csrc", name), "rb") as f:
+    for rel in ("csrc/decode_attn.hip", "csrc/decode_attn_fused_vec.hip", "csrc/qf_common.h",
+                "build.py"):
+        with open(os.path.join(ROOT, "qwenforge_amd", rel), "rb") as f:
             h.update(f.read())
     return h.hexdigest()[:16]
 

@@ -22,8 +22,8 @@ LIB_PATH = PKG / "_qf_attn.so"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
-SOURCES = ["decode_attn.hip", "prefill_attn.hip", "rope_append.hip", "decode_step.hip", "probe.hip",
-           "decode_valu.hip", "capi.cpp"]
+SOURCES = ["decode_attn.hip", "decode_attn_fused_vec.hip", "prefill_attn.hip", "rope_append.hip",
+           "decode_step.hip", "probe.hip", "decode_valu.hip", "capi.cpp"]
 # Packed-fp32 VALU forms are disabled for all device code (they have produced
 # silently wrong results on this hardware pool); hipcc's host pass warns that it
 # does not know the feature, which is harmless.
@@ -32,10 +32,17 @@ DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
                 # accumulators are rescaled, so AGPR<->VGPR copies would dominate.
                 "-mllvm", "-amdgpu-mfma-vgpr-form"]
 COMMON_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", f"-I{ROOT / 'include'}"]
+# Per-unit additions.  decode_attn_fused_vec.hip holds the decode kernel's
+# single-launch-merge instances with a 16-byte bias (the headline decode
+# shape), which run faster under LLVM's max-ILP machine scheduler (config 2
+# 6.85 vs 6.97 us per launch on MI355X) while other instances ran slower with
+# it; the flag applies to a whole unit, hence the separate file.
+UNIT_FLAGS = {"decode_attn_fused_vec.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]}
 
 
 def _compile(src: Path, obj: Path, verbose: bool) -> None:
-    cmd = [HIPCC, *COMMON_FLAGS, *DEVICE_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *COMMON_FLAGS, *DEVICE_FLAGS, *UNIT_FLAGS.get(src.name, []), "-c", str(src), "-o",
+           str(obj)]
     if src.suffix == ".cpp":
         cmd = [HIPCC, "-O3", "-std=c++17", "-fPIC", f"-I{ROOT / 'include'}",
                "-D__HIP_PLATFORM_AMD__", "-c", str(src), "-o", str(obj)]

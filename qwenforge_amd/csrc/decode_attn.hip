@@ -581,6 +581,7 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
   }
 }
 
+#ifndef QF_DECODE_FUSED_VEC_UNIT
 // Second launch of the two-kernel shape: one workgroup of four waves per
 // (b, h, query).  Thread (sub = tid / 16, d4 = tid % 16) folds partials
 // j = sub, sub + 16, ... of dims 4*d4 .. +3 (fold_wave, eight per batch);
@@ -611,15 +612,27 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
   }
 }
 
+// The single-launch-merge instances with a 16-byte bias over a contiguous
+// cache (the ragged serving batch of the headline shape) are compiled in
+// their own unit, decode_attn_fused_vec.hip, with LLVM's max-ILP machine
+// scheduler; everything else here keeps the default one.  Measured on MI355X
+// (outputs bit-identical): config 2 6.85 vs 6.97 us per launch, while the
+// same flag on the whole file made config 3 (9.95 vs 9.71) and the
+// single-launch merge without bias at B=12 L=5760 (12.05 vs 11.76) slower.
+void launch_fused_vec(const DecodeArgs& a, int nw, dim3 grid, hipStream_t st);
+
 template <int NW, int kBias, bool kPaged>
 static void launch_split(const DecodeArgs& a, int mode, dim3 grid, hipStream_t st) {
   const dim3 block(NW * 64);
-  if (mode == kDirect)
+  if (mode == kDirect) {
     hipLaunchKernelGGL((decode_split_kernel<NW, kBias, kDirect, kPaged>), grid, block, 0, st, a);
-  else if (mode == kPartial)
+  } else if (mode == kPartial) {
     hipLaunchKernelGGL((decode_split_kernel<NW, kBias, kPartial, kPaged>), grid, block, 0, st, a);
-  else
+  } else if constexpr (kBias == kBiasVec && !kPaged) {
+    launch_fused_vec(a, NW, grid, st);
+  } else {
     hipLaunchKernelGGL((decode_split_kernel<NW, kBias, kFused, kPaged>), grid, block, 0, st, a);
+  }
 }
 
 template <int NW, bool kPaged>
@@ -629,8 +642,25 @@ static void launch_nw(const DecodeArgs& a, int mode, dim3 grid, hipStream_t st) 
   else launch_split<NW, kBiasScalar, kPaged>(a, mode, grid, st);
 }
 
+#endif  // QF_DECODE_FUSED_VEC_UNIT
+
+#ifdef QF_DECODE_FUSED_VEC_UNIT
+void launch_fused_vec(const DecodeArgs& a, int nw, dim3 grid, hipStream_t st) {
+  const dim3 block(nw * 64);
+  if (nw == 16)
+    hipLaunchKernelGGL((decode_split_kernel<16, kBiasVec, kFused, false>), grid, block, 0, st, a);
+  else if (nw == 8)
+    hipLaunchKernelGGL((decode_split_kernel<8, kBiasVec, kFused, false>), grid, block, 0, st, a);
+  else if (nw == 4)
+    hipLaunchKernelGGL((decode_split_kernel<4, kBiasVec, kFused, false>), grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL((decode_split_kernel<2, kBiasVec, kFused, false>), grid, block, 0, st, a);
+}
+#endif
+
 }  // namespace qf
 
+#ifndef QF_DECODE_FUSED_VEC_UNIT
 using namespace qf;
 
 static bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -961,3 +991,5 @@ extern "C" int qf_decode_attn_noalloc(const void* q, int64_t q_sb, int64_t q_sh,
   if (mode == kPartial) launch_combine(a, st);
   return (int)hipGetLastError();
 }
+
+#endif  // QF_DECODE_FUSED_VEC_UNIT
