@@ -805,14 +805,19 @@ def traffic_summary(fetch_csv, write_csv):
 def _kernel_source_hash():
     """sha256 prefix of the decode kernel's source and build: decode_attn.hip,
     decode_attn_fused_vec.hip (the headline instances' unit), qf_common.h and
-    build.py (which holds that unit's compiler flags)."""
+    the compiler flags ``qwenforge_amd.build`` gives those two units."""
     import hashlib
 
+    from qwenforge_amd import build
+
     h = hashlib.sha256()
-    for rel in ("csrc/decode_attn.hip", "csrc/decode_attn_fused_vec.hip", "csrc/qf_common.h",
-                "build.py"):
-        with open(os.path.join(ROOT, "qwenforge_amd", rel), "rb") as f:
+    for rel in ("decode_attn.hip", "decode_attn_fused_vec.hip", "qf_common.h"):
+        with open(os.path.join(ROOT, "qwenforge_amd", "csrc", rel), "rb") as f:
             h.update(f.read())
+    flags = [build.COMMON_FLAGS[:-1], build.DEVICE_FLAGS,
+             build.UNIT_FLAGS.get("decode_attn.hip", []),
+             build.UNIT_FLAGS.get("decode_attn_fused_vec.hip", [])]
+    h.update(repr(flags).encode())
     return h.hexdigest()[:16]
 
 

@@ -32,12 +32,17 @@ DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
                 # accumulators are rescaled, so AGPR<->VGPR copies would dominate.
                 "-mllvm", "-amdgpu-mfma-vgpr-form"]
 COMMON_FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", f"-I{ROOT / 'include'}"]
-# Per-unit additions.  decode_attn_fused_vec.hip holds the decode kernel's
-# single-launch-merge instances with a 16-byte bias (the headline decode
-# shape), which run faster under LLVM's max-ILP machine scheduler (config 2
-# 6.85 vs 6.97 us per launch on MI355X) while other instances ran slower with
-# it; the flag applies to a whole unit, hence the separate file.
-UNIT_FLAGS = {"decode_attn_fused_vec.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"]}
+# Per-unit machine-scheduler choices, measured on MI355X (outputs unchanged):
+# - decode_attn_fused_vec.hip holds the decode kernel's single-launch-merge
+#   instances with a 16-byte bias (the headline decode shape), faster under
+#   max-ILP (config 2 6.85 vs 6.97 us per launch) while other instances ran
+#   slower with it; the flag applies to a whole unit, hence the separate file;
+# - decode_step.hip under max-memory-clause: the batch-1 decode step 0.5111 ->
+#   0.5085 ms, batch 4 unchanged (max-ILP and iterative-minreg cost 4-5%).
+UNIT_FLAGS = {
+    "decode_attn_fused_vec.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
+    "decode_step.hip": ["-mllvm", "-amdgpu-sched-strategy=max-memory-clause"],
+}
 
 
 def _compile(src: Path, obj: Path, verbose: bool) -> None:
