@@ -164,6 +164,27 @@ int qf_decode_split(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sg,
                     int B, int KVH, int G, int D, int cap, float scale,
                     void* stream);
 
+/*
+ * qf_decode_split over the reference's split ranges: split s covers
+ * [s*split_len, min(+split_len, cap)) with split_len = ceil(cap / S) rounded
+ * up to a multiple of 32, as _flash_decode_attention computes it
+ * (student_engine.py:851), and kv_last (optional) only masks: slots past it
+ * are read and given zero weight.  The ranges then need no device load, so
+ * the first K/V loads do not wait for kv_last.  For callers whose rows fill
+ * most of the capacity, such as a decode engine's per-layer caches (the
+ * slots past kv_last are read for nothing).  Partials have
+ * qf_decode_split's layout and meaning; a split past kv_last holds the empty
+ * state (m = -inf, l = 0, acc = 0), which every merge drops.
+ */
+int qf_decode_split_capacity(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sg,
+                             const void* k, int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                             const void* v, int64_t v_sb, int64_t v_sh, int64_t v_sn,
+                             const void* bias, int64_t bias_sb,
+                             const int64_t* kv_last, int64_t kv_last_sb,
+                             float* acc, float* m, float* l, int splits,
+                             int B, int KVH, int G, int D, int cap, float scale,
+                             void* stream);
+
 int qf_decode_combine(const float* acc, const float* m, const float* l, int splits,
                       void* out, int64_t o_sb, int64_t o_sh, int64_t o_sg,
                       int B, int KVH, int G, int D, void* stream);

@@ -51,6 +51,16 @@ SIGNATURES = {
         _i32, _i32, _i32, _i32, _i32,   # B, KVH, G, D, cap
         _f32, _vp,                      # scale, stream
     ],
+    "qf_decode_split_capacity": [
+        _vp, _i64, _i64, _i64,          # q
+        _vp, _i64, _i64, _i64,          # k
+        _vp, _i64, _i64, _i64,          # v
+        _vp, _i64,                      # bias, bias_sb
+        _vp, _i64,                      # kv_last, kv_last_sb
+        _vp, _vp, _vp, _i32,            # acc, m, l, splits
+        _i32, _i32, _i32, _i32, _i32,   # B, KVH, G, D, cap
+        _f32, _vp,                      # scale, stream
+    ],
     "qf_decode_combine": [
         _vp, _vp, _vp, _i32,            # acc, m, l, splits
         _vp, _i64, _i64, _i64,          # out, o_sb, o_sh, o_sg

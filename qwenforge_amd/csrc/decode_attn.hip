@@ -49,7 +49,8 @@ constexpr int kTile = 32;       // keys per wave iteration
 constexpr int kVtStride = 36;   // LDS row stride (halves) of a transposed V tile
 constexpr int kMaxG = 16;
 
-enum Mode { kDirect = 0, kPartial = 1, kFused = 2 };
+// kPartialCap: kPartial over the capacity split (split_range<true>).
+enum Mode { kDirect = 0, kPartial = 1, kFused = 2, kPartialCap = 3 };
 
 // Merge mode of a call with `splits` partials; `ticket`: the caller passed
 // merge counters (single launch).
@@ -84,7 +85,11 @@ struct DecodeArgs {
   int64_t t_sb, k_sp, v_sp;
   int log2p, n_pages;
 };
-
+static_assert(covers_lines(sizeof(DecodeArgs),
+                           {offsetof(DecodeArgs, q), offsetof(DecodeArgs, v),
+                            offsetof(DecodeArgs, acc), offsetof(DecodeArgs, KVH),
+                            offsetof(DecodeArgs, log2p)}),
+              "the split kernel's touch_arg_lines fields cover every line");
 // Partial-scratch store: a relaxed agent-scope atomic store, which the
 // compiler emits as a write-through (sc1) store, so a workgroup on another
 // XCD sees it without an L2 writeback.
@@ -92,22 +97,26 @@ __device__ __forceinline__ void st_wt(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Slot range [lo, hi) of split `s` for batch row `b`: the row's valid slots
-// end at upper = kv_last[b] + 1 (clamped to [0, cap]; cap without a bound)
-// and split_len = ceil(upper / S), rounded up to whole 32-key tiles.  (The
-// reference splits the capacity, split_len = ceil(cap / S) at SE:851;
-// splitting the bound keeps every split busy, and reads nothing, past the
-// newest slot.)
+// Slot range [lo, hi) that split `s` of batch row `b` reads.  By default the
+// row's valid slots end at upper = kv_last[b] + 1 (clamped to [0, cap]; cap
+// without a bound) and split_len = ceil(upper / S), rounded up to whole
+// 32-key tiles: every split stays busy and nothing past the newest slot is
+// read, but the first tile's addresses wait for the kv_last load.  kCap
+// splits the capacity as the reference does (split_len = ceil(cap / S) at
+// SE:851), so the ranges need no device load; kv_last then only masks (see
+// the kernel).  A compile-time choice: with a run-time one the ranges would
+// still wait for the load through a select.
+template <bool kCap>
 __device__ __forceinline__ void split_range(const DecodeArgs& a, int b, int s, int& lo, int& hi) {
-  int upper = a.cap;
-  if (a.kv_last != nullptr) {
+  int span = a.cap;
+  if (!kCap && a.kv_last != nullptr) {
     const int64_t last = a.kv_last[(int64_t)b * a.kv_last_sb];
-    upper = (int)(last + 1 < 0 ? 0 : (last + 1 > a.cap ? a.cap : last + 1));
+    span = (int)(last + 1 < 0 ? 0 : (last + 1 > a.cap ? a.cap : last + 1));
   }
-  int split_len = (upper + a.splits - 1) / a.splits;
+  int split_len = (span + a.splits - 1) / a.splits;
   split_len = (split_len + kTile - 1) / kTile * kTile;
   lo = s * split_len;
-  hi = lo + split_len < upper ? lo + split_len : upper;
+  hi = lo + split_len < span ? lo + split_len : span;
 }
 
 // (M, L, A) <- log-sum-exp merge of two partial states (m in natural-log
@@ -303,7 +312,8 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
 
   const int s = blockIdx.x;
   const int bh = blockIdx.y;
-  const int b = bh / a.KVH, h = bh % a.KVH;
+  const int KVH = touch_arg_lines(a.KVH, a.q, a.v, a.acc, a.log2p);
+  const int b = bh / KVH, h = bh % KVH;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: tile math stays scalar
@@ -328,8 +338,21 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     }
   }
 
+  constexpr bool kCap = kMode == kPartialCap;
   int lo, hi;
-  split_range(a, b, s, lo, hi);
+  split_range<kCap>(a, b, s, lo, hi);
+  // kCap: kv_last only masks.  It is read with a vector load (a VGPR
+  // address), issued with the q loads ahead of the first tile's, and first
+  // used in the first tile's compute: the wait for it is then an in-order
+  // vmcnt wait the tile loads behind it have not been held up by.  (A
+  // scalar load is waited for with lgkmcnt(0), which the next scalar load of
+  // a kernel argument forces before the tile loads are issued.)
+  int64_t kvl = (int64_t)a.cap - 1;
+  if (kCap && a.kv_last != nullptr) {
+    int zero = 0;
+    asm("" : "+v"(zero));
+    kvl = a.kv_last[(int64_t)b * a.kv_last_sb + zero];
+  }
 
   float m_run = kNegInf, l_run = 0.f;
   f32x4 o[4];
@@ -375,6 +398,17 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
   };
   // Scores, online softmax and PV product of one tile (keys t0 .. t0 + 31).
   const auto consume = [&](const Tile& cur, int t0) __attribute__((always_inline)) {
+    // Scores of keys at or past hv are dropped: hi, or under kCap also the
+    // slots past kv_last.  The empty asm keeps the use of kvl (and so the
+    // wait for its load) here instead of letting it be hoisted above the
+    // tile loads.
+    int hv = hi;
+    if (kCap) {
+      int64_t x = kvl;
+      asm volatile("" : "+v"(x));
+      const int upper = (int)(x + 1 < 0 ? 0 : (x + 1 > a.cap ? a.cap : x + 1));
+      hv = __builtin_amdgcn_readfirstlane(hi < upper ? hi : upper);
+    }
     // Bias of the lane's 8 keys t0 + 8*grp + jj, in log2 units.
     float bv[8];
     const int kbase = t0 + 8 * grp;
@@ -391,14 +425,22 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
 
     // Transpose V into LDS: vt[d][key - t0], four keys per 8-byte write.
     // Dim e of the four keys: the low (e even) or high half of word e / 2 of
-    // each row, paired by byte selects.
+    // each row, paired by byte selects.  Over the capacity split, rows at or
+    // past hv are whatever the cache holds there: they are zeroed, since
+    // their zero weights would not cancel a NaN or an infinity (0 * NaN).
     {
       const int m4 = 4 * (lane & 7), c8 = 8 * (lane >> 3);
+      u32x4 vr[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        vr[r] = cur.v[r];
+        if (kCap && t0 + m4 + r >= hv) vr[r] = u32x4{0u, 0u, 0u, 0u};
+      }
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const unsigned sel = (e & 1) ? 0x07060302u : 0x05040100u;
-        const u32x2 w = {__builtin_amdgcn_perm(cur.v[1][e >> 1], cur.v[0][e >> 1], sel),
-                         __builtin_amdgcn_perm(cur.v[3][e >> 1], cur.v[2][e >> 1], sel)};
+        const u32x2 w = {__builtin_amdgcn_perm(vr[1][e >> 1], vr[0][e >> 1], sel),
+                         __builtin_amdgcn_perm(vr[3][e >> 1], vr[2][e >> 1], sel)};
         *reinterpret_cast<f16x4*>(&vt[c8 + e][m4]) = __builtin_bit_cast(f16x4, w);
       }
     }
@@ -408,7 +450,7 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
     for (int jj = 0; jj < 8; ++jj) {
       float x = (jj < 4 ? c0[jj] : c1[jj - 4]) * a.scale_log2;
       if (kHasBias) x += bv[jj];
-      sc[jj] = kbase + jj < hi ? x : kNegInf;
+      sc[jj] = kbase + jj < hv ? x : kNegInf;
     }
     float mt = sc[0];
 #pragma unroll
@@ -589,7 +631,8 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
 // waves through LDS, and wave 0 writes fp16 acc / l.
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
   __shared__ float red[3][16][6];
-  const int bh = blockIdx.x / a.G, q = blockIdx.x % a.G;
+  const int G = touch_arg_lines(a.G, a.acc);  // the lines it reads
+  const int bh = blockIdx.x / G, q = blockIdx.x % G;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int d4 = lane & 15;
   float M = kNegInf, L = 0.f;
@@ -628,6 +671,9 @@ static void launch_split(const DecodeArgs& a, int mode, dim3 grid, hipStream_t s
     hipLaunchKernelGGL((decode_split_kernel<NW, kBias, kDirect, kPaged>), grid, block, 0, st, a);
   } else if (mode == kPartial) {
     hipLaunchKernelGGL((decode_split_kernel<NW, kBias, kPartial, kPaged>), grid, block, 0, st, a);
+  } else if (mode == kPartialCap) {
+    if constexpr (!kPaged)
+      hipLaunchKernelGGL((decode_split_kernel<NW, kBias, kPartialCap, false>), grid, block, 0, st, a);
   } else if constexpr (kBias == kBiasVec && !kPaged) {
     launch_fused_vec(a, NW, grid, st);
   } else {
@@ -804,6 +850,23 @@ extern "C" int qf_decode_split(const void* q, int64_t q_sb, int64_t q_sh, int64_
                            nullptr, 0, 0, 0, B, KVH, G, D, cap, scale, true, false);
   if (rc != QF_OK) return rc;
   launch_split_mode(a, kPartial, static_cast<hipStream_t>(stream));
+  return (int)hipGetLastError();
+}
+
+extern "C" int qf_decode_split_capacity(const void* q, int64_t q_sb, int64_t q_sh, int64_t q_sg,
+                                        const void* k, int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                                        const void* v, int64_t v_sb, int64_t v_sh, int64_t v_sn,
+                                        const void* bias, int64_t bias_sb,
+                                        const int64_t* kv_last, int64_t kv_last_sb,
+                                        float* acc, float* m, float* l, int splits,
+                                        int B, int KVH, int G, int D, int cap, float scale,
+                                        void* stream) {
+  DecodeArgs a;
+  const int rc = make_args(a, q, q_sb, q_sh, q_sg, k, k_sb, k_sh, k_sn, v, v_sb, v_sh, v_sn,
+                           bias, bias_sb, kv_last, kv_last_sb, acc, m, l, splits, nullptr,
+                           nullptr, 0, 0, 0, B, KVH, G, D, cap, scale, true, false);
+  if (rc != QF_OK) return rc;
+  launch_split_paging<false>(a, kPartialCap, static_cast<hipStream_t>(stream));
   return (int)hipGetLastError();
 }
 

@@ -244,6 +244,10 @@ struct QkvArgs {
   const int64_t* slots;
   int64_t slot_sb;
 };
+static_assert(covers_lines(sizeof(QkvArgs), {offsetof(QkvArgs, x), offsetof(QkvArgs, bias),
+                                             offsetof(QkvArgs, write_index), offsetof(QkvArgs, K),
+                                             offsetof(QkvArgs, slots)}),
+              "touch_arg_lines fields cover every line");
 
 // One wave per (head, d) rotate-half pair: rows head*64 + d and head*64 + d + 32.
 template <int NB, bool kPaged, bool kPos>
@@ -252,7 +256,7 @@ __global__ __launch_bounds__(kNT) void rms_qkv_rope_append_kernel(QkvArgs a) {
   __shared__ __attribute__((aligned(16))) f16 xs[NB * kMaxNormK];
   __shared__ float red[kNW * NB];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int K = a.K, C = K / 8;
+  const int K = touch_arg_lines(a.K, a.x, a.bias, a.write_index, a.slots), C = K / 8;
   const int p_raw = blockIdx.x * kNW + w;
   const bool valid = p_raw < a.n_pairs;
   const int p = valid ? p_raw : a.n_pairs - 1;  // spare waves load a real pair, store nothing
@@ -494,6 +498,8 @@ struct MergeArgs {
   int64_t h_sb;
   int K, N;
 };
+static_assert(covers_lines(sizeof(MergeArgs), {offsetof(MergeArgs, acc), offsetof(MergeArgs, K)}),
+              "touch_arg_lines fields cover every line");
 
 // The merge prologue shared by the o_proj kernels: every workgroup folds
 // all B x KVH x G x 64 merged attention values into LDS xs (fp16, the
@@ -593,7 +599,7 @@ __global__ __launch_bounds__(kNT) void attn_merge_gemv_residual_kernel(MergeArgs
   constexpr int NS = kMaxNormK / 8 / 64;
   __shared__ __attribute__((aligned(16))) f16 xs[NB * kMaxNormK];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int K = a.K, C = K / 8;
+  const int K = touch_arg_lines(a.K, a.acc), C = K / 8;
   const int n0 = (blockIdx.x * kNW + w) * RW;
   f16x8 wr[RW][NS];
   const int re = lane < RW * NB ? lane / NB : 0, be = lane < RW * NB ? lane % NB : 0;
@@ -800,7 +806,7 @@ __global__ __launch_bounds__(kNT) void attn_merge_o_proj_mfma_kernel(MergeArgs a
   __shared__ __attribute__((aligned(16))) f16 xs[NB * kMaxNormK];
   __shared__ f32x4 part[kNW][64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int K = a.K, nkb = K / 32;
+  const int K = touch_arg_lines(a.K, a.acc), nkb = K / 32;
   const int per = (nkb + kOpKS - 1) / kOpKS;
   const int kp = w % kOpKS;
   const int rb = blockIdx.x;
@@ -840,7 +846,7 @@ __global__ __launch_bounds__(kNT) void rms_qkv_rope_append_mfma_kernel(QkvArgs a
   __shared__ float red[kNW * NB];
   __shared__ f32x4 part[kNW][64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int K = a.K, nkb = K / 32;
+  const int K = touch_arg_lines(a.K, a.x, a.bias, a.write_index, a.slots), nkb = K / 32;
   const int per = (nkb + kQkvKS - 1) / kQkvKS;
   const int kp = w % kQkvKS;
   const int nrb = (a.QH + 2 * a.KVH) * 4;

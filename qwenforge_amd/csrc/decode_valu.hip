@@ -50,6 +50,8 @@ struct Args {
   int KVH, cap, splits;
   float scale_log2;
 };
+static_assert(covers_lines(sizeof(Args), {offsetof(Args, q), offsetof(Args, v), offsetof(Args, KVH)}),
+              "touch_arg_lines fields cover every line");
 
 __device__ __forceinline__ float dpp_f(float x, int ctrl) {
   // Row-local lane shuffle; ctrl is a compile-time DPP control.
@@ -112,7 +114,8 @@ __global__ __launch_bounds__(kNW * 64) void decode_split_valu_kernel(Args a) {
   __shared__ float mo[kNW][kG][kD];
   __shared__ float mm[kNW][kG], ml[kNW][kG];
 
-  const int s = blockIdx.x, bh = blockIdx.y, b = bh / a.KVH, h = bh % a.KVH;
+  const int KVH = touch_arg_lines(a.KVH, a.q, a.v, a.acc);
+  const int s = blockIdx.x, bh = blockIdx.y, b = bh / KVH, h = bh % KVH;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   for (int i = tid; i < kG * 8; i += kNW * 64) {

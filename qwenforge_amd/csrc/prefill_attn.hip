@@ -88,6 +88,11 @@ struct Args {
   int64_t t_sb;
   int log2p, n_pages, ppr;
 };
+// The fields every prefill kernel passes to touch_arg_lines (its first value
+// is B, QH or KVH, on the fourth line).
+static_assert(covers_lines(sizeof(Args), {offsetof(Args, q), offsetof(Args, v), offsetof(Args, kc),
+                                          offsetof(Args, B), offsetof(Args, snake)}),
+              "touch_arg_lines fields cover every line");
 
 // Element offset of slot `slot` of row b (kv head 0) in a cache: contiguous,
 // or through the block table (ok = false for a page outside the pool).
@@ -238,7 +243,8 @@ __global__ __launch_bounds__(kWaves * 64) void prefill_kernel(Args a) {
   const int n_mtiles = gridDim.x;
   const int mt = n_mtiles - 1 - blockIdx.x;  // heaviest tiles first
   const int bq = blockIdx.y;
-  const int b = bq / a.QH, hq = bq % a.QH;
+  const int QH = touch_arg_lines(a.QH, a.q, a.v, a.kc, a.snake);
+  const int b = bq / QH, hq = bq % QH;
   const int hk = hq / a.G;
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
@@ -668,7 +674,7 @@ __global__ __launch_bounds__(kG * 4 * 64, 4) void prefill_lds2_kernel(Args a) {
 
   // One-dimensional grid, (query tile, b * QH + q head) with the head
   // fastest and the heaviest query tiles first.
-  const int n_bq = a.B * a.QH;
+  const int n_bq = touch_arg_lines(a.B, a.q, a.v, a.kc, a.snake) * a.QH;
   const int n_mtiles = (a.S + kBM - 1) / kBM;
   // Item (query tile, head) of this workgroup; items are numbered heaviest
   // first.  With a second round (a.snake = CUs, P = grid - CUs workgroups past
@@ -858,7 +864,8 @@ __global__ __launch_bounds__(256) void rope_kv_prefill_kernel(Args a) {
   const int tok = blockIdx.x * 16 + (threadIdx.x >> 4);
   const int sub = threadIdx.x & 15;
   const int bh = blockIdx.y;
-  const int b = bh / a.KVH, h = bh % a.KVH;
+  const int KVH = touch_arg_lines(a.KVH, a.k, a.v, a.kc, a.cu);
+  const int b = bh / KVH, h = bh % KVH;
   int S;
   int64_t tok0;
   row_span(a, b, S, tok0);

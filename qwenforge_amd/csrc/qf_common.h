@@ -12,6 +12,9 @@
 // without any data movement (see the key permutation in the kernels).
 #pragma once
 
+#include <cstddef>
+#include <initializer_list>
+
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -60,6 +63,47 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0,
                                            (int)(bytes < 0x7fffffff ? bytes : 0x7fffffff),
                                            0x00020000);
+}
+
+// Returns x after taking the fields f... as SGPR inputs of one empty asm:
+// their scalar loads are issued together and waited for once, before x's
+// first use.  A kernel passes a value it needs at once as x and, from every
+// other 64-byte line of its argument block that it reads, a field it uses
+// early (covers_lines checks the choice).  Left to the compiler, a field is
+// loaded where it is first used -- behind a branch, or after an earlier wait
+// -- and the first load from each line misses the scalar cache: one more
+// dependent memory round trip before the kernel's first data load.  After the
+// batch the touched fields sit in SGPRs and the rest of their lines in the
+// scalar cache.  The asm is not volatile and has an output, so it has no side
+// effects: a volatile one counts as a possible memory write, after which the
+// compiler reads uniform global data (a bound such as kv_last) with vector
+// instead of scalar loads.  One asm for all fields: chained ones let the
+// scheduler interleave the loads with waits.
+template <typename T, typename A>
+__device__ __forceinline__ T touch_arg_lines(T x, A f1) {
+  asm("" : "+s"(x) : "s"(f1));
+  return x;
+}
+template <typename T, typename A, typename B, typename C>
+__device__ __forceinline__ T touch_arg_lines(T x, A f1, B f2, C f3) {
+  asm("" : "+s"(x) : "s"(f1), "s"(f2), "s"(f3));
+  return x;
+}
+template <typename T, typename A, typename B, typename C, typename D>
+__device__ __forceinline__ T touch_arg_lines(T x, A f1, B f2, C f3, D f4) {
+  asm("" : "+s"(x) : "s"(f1), "s"(f2), "s"(f3), "s"(f4));
+  return x;
+}
+
+// True if every 64-byte line of a `bytes`-byte argument block holds one of
+// the field offsets (a touch_arg_lines choice that leaves no line out).
+constexpr bool covers_lines(size_t bytes, std::initializer_list<size_t> offsets) {
+  for (size_t line = 0; 64 * line < bytes; ++line) {
+    bool hit = false;
+    for (size_t o : offsets) hit = hit || o / 64 == line;
+    if (!hit) return false;
+  }
+  return true;
 }
 
 // s_waitcnt vmcnt(n) for n in {0, 4}, leaving the other counters alone.

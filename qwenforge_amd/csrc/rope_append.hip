@@ -43,10 +43,13 @@ struct Args {
   const int64_t* slots;
   int64_t slot_sb;
 };
+static_assert(covers_lines(sizeof(Args), {offsetof(Args, q), offsetof(Args, cos),
+                                          offsetof(Args, write_index), offsetof(Args, cap)}),
+              "touch_arg_lines fields cover every line");
 
 template <bool kPaged>
 __global__ __launch_bounds__(256) void rope_append_kernel(Args a) {
-  const int b = blockIdx.x;
+  const int b = touch_arg_lines((int)blockIdx.x, a.q, a.cos, a.write_index, a.cap);
   // Element offsets of row b's destination slot (kv head 0) in the caches.
   int64_t kro, vro;
   bool in_range;

@@ -312,20 +312,25 @@ def flash_decode_attention(grouped: torch.Tensor, key_cache: torch.Tensor,
 
 
 def flash_decode_split(grouped, key_cache, value_cache, attn_bias, flash, kv_last=None,
-                       scale=None):
+                       scale=None, split_capacity=False):
     """The split launch alone (``_flash_decode_split_kernel``, SE:32-115 / SE:854-865):
-    fills the partials ``flash[0:3]`` = (acc, m, l)."""
+    fills the partials ``flash[0:3]`` = (acc, m, l).
+
+    ``split_capacity``: split the capacity as the reference does (SE:851)
+    with ``kv_last`` as a mask only (``qf_decode_split_capacity``), so the
+    first loads do not wait for it -- for rows that fill most of the cache."""
     acc, m, l, out, _, splits, cap, kv_last_sb = _decode_args(
         grouped, key_cache, value_cache, attn_bias, flash, kv_last)
     b, kvh, g, d = grouped.shape
     scale = d ** -0.5 if scale is None else scale
     lib = _lib.load()
+    name = "qf_decode_split_capacity" if split_capacity else "qf_decode_split"
     with torch.cuda.device(grouped.device):
-        rc = lib.qf_decode_split(
+        rc = getattr(lib, name)(
             *_qkv_bias_args(grouped, key_cache, value_cache, attn_bias, kv_last, kv_last_sb),
             acc.data_ptr(), m.data_ptr(), l.data_ptr(), splits,
             b, kvh, g, d, cap, float(scale), _stream(grouped.device))
-    _lib.check(rc, "qf_decode_split")
+    _lib.check(rc, name)
     return acc, m, l
 
 
