@@ -312,7 +312,9 @@ __global__ __launch_bounds__(NW * 64) void decode_split_kernel(DecodeArgs a) {
 
   const int s = blockIdx.x;
   const int bh = blockIdx.y;
-  const int KVH = touch_arg_lines(a.KVH, a.q, a.v, a.acc, a.log2p);
+  // The fields the first loads depend on (q, the kv_last bound, K/V and the
+  // bias rows), one from each further line (acc, log2p).
+  const int KVH = touch_arg_lines(a.KVH, a.q, a.v, a.bias, a.kv_last, a.kv_last_sb, a.acc, a.log2p);
   const int b = bh / KVH, h = bh % KVH;
   const int tid = threadIdx.x;
   const int lane = tid & 63;

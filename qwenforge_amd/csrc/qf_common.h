@@ -69,7 +69,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
 // their scalar loads are issued together and waited for once, before x's
 // first use.  A kernel passes a value it needs at once as x and, from every
 // other 64-byte line of its argument block that it reads, a field it uses
-// early (covers_lines checks the choice).  Left to the compiler, a field is
+// early (covers_lines checks the choice), plus any further field its first
+// data loads depend on (each later field load waits for a scalar-cache hit).  Left to the compiler, a field is
 // loaded where it is first used -- behind a branch, or after an earlier wait
 // -- and the first load from each line misses the scalar cache: one more
 // dependent memory round trip before the kernel's first data load.  After the
@@ -92,6 +93,13 @@ __device__ __forceinline__ T touch_arg_lines(T x, A f1, B f2, C f3) {
 template <typename T, typename A, typename B, typename C, typename D>
 __device__ __forceinline__ T touch_arg_lines(T x, A f1, B f2, C f3, D f4) {
   asm("" : "+s"(x) : "s"(f1), "s"(f2), "s"(f3), "s"(f4));
+  return x;
+}
+
+template <typename T, typename A, typename B, typename C, typename D, typename E, typename F,
+          typename G>
+__device__ __forceinline__ T touch_arg_lines(T x, A f1, B f2, C f3, D f4, E f5, F f6, G f7) {
+  asm("" : "+s"(x) : "s"(f1), "s"(f2), "s"(f3), "s"(f4), "s"(f5), "s"(f6), "s"(f7));
   return x;
 }
 
