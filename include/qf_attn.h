@@ -54,10 +54,11 @@ extern "C" {
 /* Human-readable text for a return code of any qf_* entry point. */
 const char* qf_error_string(int code);
 
-/* ABI version (major * 100 + minor): 300.  Changes from 200:
- * qf_attn_merge_o_proj and qf_rms_lm_head (qf_step.h) take w_layout after
- * the weight pointer, and the qf_decode_attn ticket holds one int32 counter
- * per (b, kv head) instead of one in total. */
+/* ABI version (major * 100 + minor): 301.  301 adds qf_decode_split_capacity
+ * (nothing else changes).  300, from 200: qf_attn_merge_o_proj and
+ * qf_rms_lm_head (qf_step.h) take w_layout after the weight pointer, and the
+ * qf_decode_attn ticket holds one int32 counter per (b, kv head) instead of
+ * one in total. */
 int qf_abi_version(void);
 
 /*

@@ -15,7 +15,8 @@ extern "C" const char* qf_error_string(int code) {
   return "unknown error";
 }
 
-// major * 100 + minor.  300: qf_attn_merge_o_proj and qf_rms_lm_head take a
-// weight-layout argument, and the single-launch decode ticket is one counter
-// per (b, kv head).  200: the prefill workspace entry points were removed.
-extern "C" int qf_abi_version(void) { return 300; }
+// major * 100 + minor.  301: qf_decode_split_capacity added.  300:
+// qf_attn_merge_o_proj and qf_rms_lm_head take a weight-layout argument, and
+// the single-launch decode ticket is one counter per (b, kv head).  200: the
+// prefill workspace entry points were removed.
+extern "C" int qf_abi_version(void) { return 301; }

@@ -41,7 +41,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_version_and_error_strings():
     lib = _lib.load()
-    assert lib.qf_abi_version() == 300
+    assert lib.qf_abi_version() == 301
     assert lib.qf_error_string(0) == b"success"
     assert b"invalid" in lib.qf_error_string(-1)
     assert b"unsupported" in lib.qf_error_string(-2)
