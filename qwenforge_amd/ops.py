@@ -103,7 +103,8 @@ def decode_plan(batch: int, kv_heads: int, length: int,
       splits (5.46 us against 5.58 at 8 and 6.23 for 16 split + combine);
       B=1, L=2048: 16 (6.23 against 6.47 for 64 split + combine); config 2
       (B=4, cap 2048, ragged with a bias): 16 (7.00 against 7.31 for 32 split
-      + combine).  With more pairs, splits of 128 keys, at most 192
+      + combine; re-measured single launches: 16 6.83-6.85, 8 7.34-7.35, 12
+      6.91, 20 7.33, 24 7.49, 32 8.06).  With more pairs, splits of 128 keys, at most 192
       workgroups -- e.g. B=8, L=512: 4 (6.55 against 6.72 for 16 split +
       combine);
     * longer rows: split + combine launches with one workgroup per CU
