@@ -88,10 +88,13 @@ struct Args {
   int64_t t_sb;
   int log2p, n_pages, ppr;
 };
-// The fields every prefill kernel passes to touch_arg_lines (its first value
-// is B, QH or KVH, on the fourth line).
+// The fields the attention kernels (q, v, kc, B or QH, snake) and the
+// pre-pass (k, v, kc, KVH, cu) pass to touch_arg_lines.
 static_assert(covers_lines(sizeof(Args), {offsetof(Args, q), offsetof(Args, v), offsetof(Args, kc),
                                           offsetof(Args, B), offsetof(Args, snake)}),
+              "touch_arg_lines fields cover every line");
+static_assert(covers_lines(sizeof(Args), {offsetof(Args, k), offsetof(Args, v), offsetof(Args, kc),
+                                          offsetof(Args, KVH), offsetof(Args, cu)}),
               "touch_arg_lines fields cover every line");
 
 // Element offset of slot `slot` of row b (kv head 0) in a cache: contiguous,

@@ -70,16 +70,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
 // first use.  A kernel passes a value it needs at once as x and, from every
 // other 64-byte line of its argument block that it reads, a field it uses
 // early (covers_lines checks the choice), plus any further field its first
-// data loads depend on (each later field load waits for a scalar-cache hit).  Left to the compiler, a field is
-// loaded where it is first used -- behind a branch, or after an earlier wait
-// -- and the first load from each line misses the scalar cache: one more
-// dependent memory round trip before the kernel's first data load.  After the
-// batch the touched fields sit in SGPRs and the rest of their lines in the
-// scalar cache.  The asm is not volatile and has an output, so it has no side
-// effects: a volatile one counts as a possible memory write, after which the
-// compiler reads uniform global data (a bound such as kv_last) with vector
-// instead of scalar loads.  One asm for all fields: chained ones let the
-// scheduler interleave the loads with waits.
+// data loads depend on (each later field load waits for a scalar-cache hit).
+// Left to the compiler, a field is loaded where it is first used -- behind a
+// branch, or after an earlier wait -- and the first load from each line
+// misses the scalar cache: one more dependent memory round trip before the
+// kernel's first data load.  After the batch the touched fields sit in SGPRs
+// and the rest of their lines in the scalar cache.  The asm is not volatile
+// and has an output, so it has no side effects: a volatile one counts as a
+// possible memory write, after which the compiler reads uniform global data
+// (a bound such as kv_last) with vector instead of scalar loads.  One asm for
+// all fields: chained ones let the scheduler interleave the loads with waits.
 template <typename T, typename A>
 __device__ __forceinline__ T touch_arg_lines(T x, A f1) {
   asm("" : "+s"(x) : "s"(f1));
@@ -95,7 +95,6 @@ __device__ __forceinline__ T touch_arg_lines(T x, A f1, B f2, C f3, D f4) {
   asm("" : "+s"(x) : "s"(f1), "s"(f2), "s"(f3), "s"(f4));
   return x;
 }
-
 template <typename T, typename A, typename B, typename C, typename D, typename E, typename F,
           typename G>
 __device__ __forceinline__ T touch_arg_lines(T x, A f1, B f2, C f3, D f4, E f5, F f6, G f7) {
