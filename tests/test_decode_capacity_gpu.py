@@ -116,3 +116,25 @@ def test_bound_past_capacity_is_clamped(dev):
     _, out = _split(case, dev, 8, kv_last)
     expect = oracle.grouped_decode_attention(case.grouped, case.key_cache, case.value_cache, None)
     assert (out - expect).abs().max().item() <= TOL
+
+
+@pytest.mark.parametrize("groups", [1, 4, 16])
+def test_group_sizes_and_kv_heads(dev, groups):
+    """G query heads per kv head other than 7, three kv heads, a shared bound
+    mid-row with NaN past it, split counts that leave empty splits."""
+    gen = torch.Generator("cpu").manual_seed(100 + groups)
+    cap, last = 700, 421
+    q = torch.randn(2, 3, groups, 64, generator=gen).half()
+    k = torch.randn(2, 3, cap, 64, generator=gen).half()
+    v = torch.randn(2, 3, cap, 64, generator=gen).half()
+    case = workloads.DecodeCase(q, k, v, None, [cap, cap])
+    _plant_nan(case, [last, last])
+    kv_last = torch.tensor([last], dtype=torch.int64, device=dev)
+    for splits in (3, 11):
+        got, out = _split(case, dev, splits, kv_last)
+        ref = oracle.split_partials(case.grouped, case.key_cache, case.value_cache, None, splits,
+                                    split_len=_split_len(cap, splits), upper=last + 1)
+        _check_partials(got, ref)
+        expect = oracle.grouped_decode_attention(case.grouped, case.key_cache[:, :, :last + 1],
+                                                 case.value_cache[:, :, :last + 1], None)
+        assert (out - expect).abs().max().item() <= TOL, splits
